@@ -1,0 +1,198 @@
+"""Decode-step benchmark: device us/step and tok/s of the MI355X task-graph
+decoder vs the 1.19 GB HBM weight floor.
+
+Workload (the metric's headline case): Qwen3-0.6B
+geometry, random-init bf16 weights (seed 0), batch 1, one random start token,
+greedy decode with the token fed back on the device (no host round trip), so
+the context grows 1 -> K. A "step" is one decode step of the batch. Timed: K
+back-to-back steps on one stream between a synchronize on each side, after W
+warmup steps (the state is reset to the start token before the timed run).
+
+Printed JSON line (one): value = tok/s (= batch * K / time); roofline = the
+persistent decode kernel's algorithmic bytes per launch over its average
+launch duration from HIP events recorded around every launch of the timed
+region (same stream); cpu_baseline = the CPU oracle timed on a bounded sample
+on this host. Extra keys: per-mode and per-batch ("sweep") device us/step of
+the persistent kernel vs the captured per-op hipGraph, same kernels.
+
+One GPU only: --gpus N > 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "decode-fusion-boundary_amd"))
+sys.path.insert(0, ROOT)
+
+WEIGHT_BYTES = 1_192_099_840           # model_spec.QWEN3_06B.weight_bytes()
+KV_BYTES_PER_POS = 114_688             # 28 layers * (K+V) * 1024 * 2 B
+EMBED_ROW_BYTES = 2048
+HBM_PEAK_GBPS = 8000.0
+VOCAB = 151936
+
+
+def step_bytes(contexts: list[int]) -> int:
+    """Algorithmic HBM bytes of one decode step: all weights once, each row's KV
+    (ctx positions incl. the new one) read, its new K/V written, its embedding row."""
+
+    return WEIGHT_BYTES + sum(KV_BYTES_PER_POS * c + KV_BYTES_PER_POS + EMBED_ROW_BYTES for c in contexts)
+
+
+def build_decoder(num_layers=28, num_blocks=64, launch="persistent"):
+    import torch
+    from nanovllm.backends.megakernel.taskgraph import TaskGraphDecoder
+    from nanovllm.backends.megakernel.weights import weights_from_synthetic
+    from nanovllm.synthetic import make_weights
+
+    synth = make_weights(seed=0, num_layers=num_layers)
+    w = weights_from_synthetic(synth, device="cuda")
+    kv = torch.zeros(2, num_layers, num_blocks, 256, 8, 128, dtype=torch.bfloat16, device="cuda")
+    dec = TaskGraphDecoder(w, k_cache=kv[0], v_cache=kv[1], block_size=256, num_cache_blocks=num_blocks,
+                           max_model_len=2048, launch=launch)
+    return synth, w, kv, dec
+
+
+def time_decode(dec, batch: int, start_ctx: list[int], steps: int, warmup: int, mode: str, seed: int = 0,
+                per_launch_events: bool = False):
+    """Returns (seconds for `steps` steps, per-launch durations in ms or None, contexts per step)."""
+
+    import torch
+
+    gen = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, VOCAB, (batch,), generator=gen, dtype=torch.int64).cuda()
+    pos = torch.tensor(start_ctx, dtype=torch.int64).cuda()
+    pages = 8
+    tables = torch.tensor([[b * pages + j for j in range(pages)] for b in range(batch)], dtype=torch.int32).cuda()
+    max_ctx = max(start_ctx) + max(steps, warmup) + 1
+    run = dec.prepare_steps(batch, max_ctx, mode=mode)
+    dec.stage_rows(ids, pos, tables)
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    dec.check_device_error()
+    dec.stage_rows(ids, pos, tables)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    events = []
+    if per_launch_events:
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        if per_launch_events:
+            events[i][0].record(stream)
+        run()
+        if per_launch_events:
+            events[i][1].record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    dec.check_device_error()
+    durs = [a.elapsed_time(b) for a, b in events] if per_launch_events else None
+    contexts = [[c + 1 + i for c in start_ctx] for i in range(steps)]
+    return elapsed, durs, contexts
+
+
+def cpu_baseline(sample_steps: int = 3):
+    """The CPU oracle (a restatement of the reference torch decode) on this host."""
+
+    import torch
+    from nanovllm.synthetic import make_weights
+    from oracle.qwen3_oracle import Oracle
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    synth = make_weights(seed=0, num_layers=28)
+    oracle = Oracle(synth)
+    kc = torch.zeros(28, 2, 256, 8, 128, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    tok = 42
+    oracle.decode_step([tok], [0], [[0]], kc, vc)  # warm
+    t0 = time.perf_counter()
+    for i in range(sample_steps):
+        _, toks = oracle.decode_step([tok], [i + 1], [[0]], kc, vc)
+        tok = toks[0]
+    dt = time.perf_counter() - t0
+    return {"value": sample_steps / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{sample_steps} greedy decode steps, batch 1, ctx 2..{sample_steps + 1}, full 28-layer "
+                      f"model, torch CPU fp32-accumulate restatement (oracle/qwen3_oracle.py)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mode", default="persistent", choices=["persistent", "graph"])
+    ap.add_argument("--only-kernel", action="store_true", help="timed loop only (for profilers)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the decode step runs TP=1 on a single MI355X; "
+              "multi-GPU data parallelism is independent replicas (see DESIGN.md). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    _, _, _, dec = build_decoder(num_blocks=8 * 8 + 8)
+    start = [0] * args.batch
+    elapsed, durs, contexts = time_decode(dec, args.batch, start, args.steps, args.warmup, args.mode,
+                                          per_launch_events=True)
+    if args.only_kernel:
+        print(json.dumps({"ms_per_step": elapsed * 1e3 / args.steps}))
+        return
+    ms_per_step = elapsed * 1e3 / args.steps
+    avg_launch_ms = sum(durs) / len(durs)
+    bytes_per_launch = sum(step_bytes(c) for c in contexts) / len(contexts)
+    achieved = bytes_per_launch / (avg_launch_ms * 1e-3) / 1e9
+    result = {
+        "metric": "device us/decode-step & tok/s at batch 1-8 vs 1.19GB HBM weight floor",
+        "value": round(args.batch * args.steps / elapsed, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "us_per_step": round(ms_per_step * 1e3, 2),
+        "weight_floor_us_at_8TBps": round(WEIGHT_BYTES / HBM_PEAK_GBPS / 1e3, 2),
+        "x_floor": round(ms_per_step * 1e3 / (WEIGHT_BYTES / HBM_PEAK_GBPS / 1e3), 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init bf16 weights seed 0, random start token)",
+        "config": {"workload": "C3: Qwen3-0.6B geometry decode, batch %d, context 1->%d, greedy, "
+                               "device-resident token feedback" % (args.batch, args.steps),
+                   "model": "Qwen3-0.6B geometry (random init)", "global_batch": args.batch,
+                   "seq_len": args.steps, "parallelism": "single GPU (tp1)", "launch": args.mode},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "k_persistent<1> (one launch per decode step)",
+                     "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_ms * 1e3, 2)},
+    }
+    if not args.no_sweep:
+        sweep = {}
+        for mode in ("persistent", "graph"):
+            for b in (1, 2, 4, 8):
+                el, d2, ctxs = time_decode(dec, b, [0] * b, 32, 4, mode, per_launch_events=True)
+                us = sum(d2) / len(d2) * 1e3
+                sweep[f"{mode}_b{b}"] = {"us_per_step": round(us, 2), "tok_per_s": round(b / us * 1e6, 1),
+                                         "GBps": round(sum(step_bytes(c) for c in ctxs) / len(ctxs) / us / 1e3, 1)}
+        result["sweep"] = sweep
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    dec.close()
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

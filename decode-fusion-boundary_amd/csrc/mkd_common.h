@@ -1,0 +1,142 @@
+// mkd_common.h -- constants and device helpers of the MI355X decode-step kernels.
+//
+// Coherence protocol used by every task (measured on MI355X, 8 XCDs with
+// private L2s): activations exchanged between workgroups inside one launch are
+// written and read with relaxed agent-scope atomic accesses, which the
+// compiler emits as sc1 global loads/stores (coherent across XCDs without any
+// L2 writeback/invalidate). A producer drains its stores with s_waitcnt before
+// it arrives on a counter; a consumer issues its loads only after it has seen
+// the counter. Agent-scope fences are avoided on purpose: each one costs an L2
+// writeback or invalidate (~1.7 us measured).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mkd_abi.h"
+
+namespace mkd {
+
+constexpr int H = MKD_HIDDEN;
+constexpr int I = MKD_INTERMEDIATE;
+constexpr int NQ = MKD_NUM_Q_HEADS;
+constexpr int NKV = MKD_NUM_KV_HEADS;
+constexpr int HD = MKD_HEAD_DIM;
+constexpr int QS = NQ * HD;            // 2048
+constexpr int KVS = NKV * HD;          // 1024
+constexpr int QKV_N = QS + 2 * KVS;    // 4096
+constexpr int V = MKD_VOCAB;
+constexpr int MAXB = MKD_MAX_BATCH;
+constexpr int MAXS = MKD_MAX_SPLITS;
+constexpr int GROUP = NQ / NKV;        // 2 query heads per KV head
+constexpr int NT = 256;                // threads per workgroup (4 waves)
+constexpr int NWAVE = NT / 64;
+constexpr float EPS = 1e-6f;
+constexpr int PART_STRIDE = GROUP * HD + 2 * GROUP;  // floats per attention partial
+
+// ---- workspace layout (byte offsets) -------------------------------------
+constexpr size_t OFF_RESID = 0;                                   // bf16 [2][MAXB][H]
+constexpr size_t OFF_HID_A = OFF_RESID + 2ull * MAXB * H * 2;     // bf16 [MAXB][H]  o_proj out
+constexpr size_t OFF_HID_F = OFF_HID_A + 1ull * MAXB * H * 2;     // bf16 [MAXB][H]  down out
+constexpr size_t OFF_QKV = OFF_HID_F + 1ull * MAXB * H * 2;       // bf16 [MAXB][QKV_N]
+constexpr size_t OFF_ATTN = OFF_QKV + 1ull * MAXB * QKV_N * 2;    // bf16 [MAXB][QS]
+constexpr size_t OFF_ACT = OFF_ATTN + 1ull * MAXB * QS * 2;       // bf16 [MAXB][I]
+constexpr size_t OFF_APART = OFF_ACT + 1ull * MAXB * I * 2;       // f32 [MAXB][NKV][MAXS][PART_STRIDE]
+constexpr size_t OFF_LMPART = OFF_APART + 4ull * MAXB * NKV * MAXS * PART_STRIDE;  // {f32,i32} [slots][MAXB]
+constexpr size_t OFF_CTR = OFF_LMPART + 8ull * MKD_MAX_LM_SLOTS * MAXB;
+// Counters: one 128-byte line each. Line 0 = error word. Fan-in counters own 8
+// consecutive lines (one per XCD-spread sub-slot); ticket counters own one.
+constexpr int CTR_LINE_U32 = 32;
+constexpr int CTR_ERR = 0;
+constexpr int CTR_LM_TICKET = 1;
+constexpr int CTR_COMB_BASE = 2;                                   // [layers][MAXB][NKV] tickets
+constexpr int CTR_FANIN_BASE = CTR_COMB_BASE + MKD_NUM_LAYERS * MAXB * NKV;
+constexpr int FANIN_PER_LAYER = NKV + 4;                           // qkv[h], attn, oproj, gateup, down
+constexpr int FANIN_SUBSLOTS = 8;
+constexpr int NUM_FANIN = MKD_NUM_LAYERS * FANIN_PER_LAYER;
+constexpr int NUM_CTR_LINES = CTR_FANIN_BASE + NUM_FANIN * FANIN_SUBSLOTS;
+constexpr size_t WORKSPACE_BYTES = OFF_CTR + 128ull * NUM_CTR_LINES;
+
+// Error codes written to the error word.
+constexpr uint32_t ERR_TIMEOUT = 1;
+constexpr uint32_t ERR_BAD_INST = 2;
+constexpr uint32_t ERR_BAD_INPUT = 3;  // position / block id / token id out of range
+
+// ---- bf16 --------------------------------------------------------------------
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+__device__ __forceinline__ float bf2f(uint32_t b16) { return __uint_as_float(b16 << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even fp32 -> bf16 (torch's rounding), NaN kept quiet.
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+
+// a.lo*b.lo + a.hi*b.hi + c in fp32 (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+__device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float c) {
+  c = dot2(a.x, b.x, c);
+  c = dot2(a.y, b.y, c);
+  c = dot2(a.z, b.z, c);
+  return dot2(a.w, b.w, c);
+}
+
+// ---- coherent (cross-XCD) accesses ------------------------------------------
+template <typename T>
+__device__ __forceinline__ T ld_co(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void st_co(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t add_co(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this wave's outstanding memory operations have completed.
+__device__ __forceinline__ void drain() { __builtin_amdgcn_s_waitcnt(0); }
+
+// ---- wave reductions (wave64) --------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// ---- workspace views -----------------------------------------------------------
+struct Ws {
+  uint8_t* base;
+  __device__ __forceinline__ uint16_t* resid(int i) const {
+    return reinterpret_cast<uint16_t*>(base + OFF_RESID) + (size_t)(i & 1) * MAXB * H;
+  }
+  __device__ __forceinline__ uint16_t* hid_a() const { return reinterpret_cast<uint16_t*>(base + OFF_HID_A); }
+  __device__ __forceinline__ uint16_t* hid_f() const { return reinterpret_cast<uint16_t*>(base + OFF_HID_F); }
+  __device__ __forceinline__ uint16_t* qkv() const { return reinterpret_cast<uint16_t*>(base + OFF_QKV); }
+  __device__ __forceinline__ uint16_t* attn() const { return reinterpret_cast<uint16_t*>(base + OFF_ATTN); }
+  __device__ __forceinline__ uint16_t* act() const { return reinterpret_cast<uint16_t*>(base + OFF_ACT); }
+  __device__ __forceinline__ float* apart(int b, int h, int s) const {
+    return reinterpret_cast<float*>(base + OFF_APART) + (((size_t)b * NKV + h) * MAXS + s) * PART_STRIDE;
+  }
+  __device__ __forceinline__ uint2* lmpart(int slot) const {
+    return reinterpret_cast<uint2*>(base + OFF_LMPART) + (size_t)slot * MAXB;
+  }
+  __device__ __forceinline__ uint32_t* line(int i) const {
+    return reinterpret_cast<uint32_t*>(base + OFF_CTR) + (size_t)i * CTR_LINE_U32;
+  }
+};
+
+}  // namespace mkd

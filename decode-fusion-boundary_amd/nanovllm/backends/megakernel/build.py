@@ -1,0 +1,79 @@
+"""Build of the HIP decode-step library (``libmkd_decode.so``), in-tree.
+
+The reference JIT-compiles a torch extension with nvcc
+(``backends/megakernel/build.py:59-93``). Here the kernels are plain HIP
+compiled once by ``hipcc`` for gfx950 into a C-ABI shared library next to this
+file; Python binds it with ctypes (:mod:`.native`). Build flags:
+
+* ``--offload-arch=gfx950 -O3 -std=c++17 -fPIC -shared``;
+* ``-Xclang -target-feature -Xclang -packed-fp32-ops`` keeps packed-FP32 VALU
+  instructions out of the generated code;
+* ``MKD_ARCH`` overrides the architecture (for experiments only).
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+PKG_ROOT = HERE.parents[2]          # decode-fusion-boundary_amd/
+REPO_ROOT = PKG_ROOT.parent
+CSRC = PKG_ROOT / "csrc"
+INCLUDE = REPO_ROOT / "include"
+LIB_NAME = "libmkd_decode.so"
+LIB_PATH = HERE / LIB_NAME
+SOURCES = ("mkd_decode.hip",)
+HEADERS = ("mkd_common.h", "mkd_tasks.h")
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    path = Path(rocm) / "bin" / "hipcc"
+    return str(path) if path.exists() else "hipcc"
+
+
+def compile_command(out: Path = LIB_PATH) -> list[str]:
+    arch = os.environ.get("MKD_ARCH", "gfx950")
+    return [
+        hipcc(),
+        f"--offload-arch={arch}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        f"-I{INCLUDE}",
+        "-o", str(out),
+        *[str(CSRC / s) for s in SOURCES],
+    ]
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the library (always; the caller decides when to rebuild)."""
+
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = compile_command(tmp)
+    if verbose:
+        print(" ".join(cmd))
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def library_path() -> Path:
+    return LIB_PATH
+
+
+def get_extension():
+    """Load the built library (build it if it is missing). Mirrors the reference
+    ``get_extension()`` entry point name."""
+
+    from . import native
+
+    if not LIB_PATH.exists():
+        build()
+    return native.load()

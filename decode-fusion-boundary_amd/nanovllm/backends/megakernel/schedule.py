@@ -1,0 +1,278 @@
+"""Task-graph generator for one Qwen3 decode step (host side, pure Python).
+
+Counterpart of the reference ``backends/megakernel/schedule.py``
+(``build_schedule`` :1102-1165, wave builders :718-1001, ``place_round_robin``
+:1040-1055, ``serialize_inst_buf`` :1063-1082), redesigned for the MI355X
+kernels in ``csrc/mkd_tasks.h``:
+
+* one task = one workgroup-sized unit; GEMV stages are split into row blocks
+  so that a stage has about one task per compute unit (16 QKV rows, 4 O rows,
+  12 gate/up channel pairs, 4 down rows, ~594 LM-head rows at 256 CUs);
+* QKV row blocks never straddle a KV head's rows (q: 256 rows, k/v: 128 each
+  per KV head), so attention of head ``h`` waits only on head ``h``'s blocks;
+* dependencies are fan-in counters: a task waits until a counter reaches the
+  number of producer tasks and arrives on one counter when done; the split-KV
+  partials of one (row, head) are merged by their last arriving split, which
+  alone arrives on the layer's attention counter;
+* placement is round-robin with a cursor carried across stages; each
+  workgroup's row is in global stage order, which makes the graph
+  deadlock-free by construction (checked by :mod:`.verifier`).
+
+Instruction words: ``[op, layer, a0, a1, a2, wait, wait_count, signal]``
+(``include/mkd_abi.h``). Fan-in counter ids: ``layer * 12 + k`` with
+k = 0..7 the QKV blocks of KV head k, 8 attention, 9 O-proj, 10 gate/up,
+11 down.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+from .native import (
+    INST_WORDS, MAX_BATCH, MAX_LM_SLOTS, MAX_SPLITS, OP_ATTN, OP_DOWN, OP_GATEUP,
+    OP_LMHEAD, OP_OPROJ, OP_QKV,
+)
+
+HIDDEN = 1024
+INTERMEDIATE = 3072
+NUM_Q_HEADS = 16
+NUM_KV_HEADS = 8
+HEAD_DIM = 128
+Q_SIZE = NUM_Q_HEADS * HEAD_DIM
+KV_SIZE = NUM_KV_HEADS * HEAD_DIM
+QKV_ROWS = Q_SIZE + 2 * KV_SIZE
+VOCAB = 151936
+NUM_LAYERS = 28
+FANIN_PER_LAYER = NUM_KV_HEADS + 4
+BATCH_BUCKETS = (1, 2, 4, 8)
+
+
+def fanin_qkv(layer: int, kv_head: int) -> int:
+    return layer * FANIN_PER_LAYER + kv_head
+
+
+def fanin_attn(layer: int) -> int:
+    return layer * FANIN_PER_LAYER + NUM_KV_HEADS
+
+
+def fanin_oproj(layer: int) -> int:
+    return layer * FANIN_PER_LAYER + NUM_KV_HEADS + 1
+
+
+def fanin_gateup(layer: int) -> int:
+    return layer * FANIN_PER_LAYER + NUM_KV_HEADS + 2
+
+
+def fanin_down(layer: int) -> int:
+    return layer * FANIN_PER_LAYER + NUM_KV_HEADS + 3
+
+
+def batch_bucket(rows: int) -> int:
+    for b in BATCH_BUCKETS:
+        if rows <= b:
+            return b
+    raise ValueError(f"batch {rows} exceeds the compiled maximum {MAX_BATCH}")
+
+
+def auto_attn_splits(max_context: int, minimum: int = 1) -> int:
+    """Split-KV factor: one split per 256 cached positions, power of two, <= 16."""
+
+    want = max(1, -(-int(max_context) // 256))
+    splits = 1
+    while splits < want and splits < MAX_SPLITS:
+        splits *= 2
+    return max(min(int(minimum), MAX_SPLITS), splits)
+
+
+@dataclass(frozen=True)
+class Task:
+    op: int
+    layer: int
+    a0: int
+    a1: int = 0
+    a2: int = 0
+    wait: int = -1
+    wait_count: int = 0
+    signal: int = -1
+
+    def words(self) -> list[int]:
+        return [self.op, self.layer, self.a0, self.a1, self.a2, self.wait,
+                self.wait_count, self.signal]
+
+
+@dataclass
+class Stage:
+    op: int
+    layer: int
+    tasks: list[Task] = field(default_factory=list)
+
+
+@dataclass
+class Schedule:
+    batch: int
+    attn_splits: int
+    num_layers: int
+    grid: int
+    stages: list[Stage]
+    rows: list[list[Task]]          # per workgroup, in execution order
+
+    @property
+    def num_tasks(self) -> int:
+        return sum(len(s.tasks) for s in self.stages)
+
+    @property
+    def max_inst(self) -> int:
+        return max(1, max(len(r) for r in self.rows))
+
+    @property
+    def lm_slots(self) -> int:
+        return sum(len(s.tasks) for s in self.stages if s.op == OP_LMHEAD)
+
+    def persistent_words(self) -> tuple[list[int], list[int]]:
+        """``[grid][max_inst][8]`` flattened (NOP-padded) and ``num_inst[grid]``."""
+
+        flat: list[int] = []
+        pad = [0] * INST_WORDS
+        for row in self.rows:
+            for t in row:
+                flat.extend(t.words())
+            for _ in range(self.max_inst - len(row)):
+                flat.extend(pad)
+        return flat, [len(r) for r in self.rows]
+
+    def stage_words(self) -> tuple[list[int], list[tuple[int, int, int, int]]]:
+        """Instruction list in stage order and ``(op, layer, first, count)`` per stage."""
+
+        flat: list[int] = []
+        table = []
+        first = 0
+        for st in self.stages:
+            for t in st.tasks:
+                flat.extend(t.words())
+            table.append((st.op, st.layer, first, len(st.tasks)))
+            first += len(st.tasks)
+        return flat, table
+
+
+def split_range(start: int, length: int, pieces: int) -> list[tuple[int, int]]:
+    """Split ``[start, start+length)`` into ``pieces`` near-equal (first, count) blocks."""
+
+    pieces = max(1, min(pieces, length))
+    base, extra = divmod(length, pieces)
+    out = []
+    cur = start
+    for i in range(pieces):
+        n = base + (1 if i < extra else 0)
+        out.append((cur, n))
+        cur += n
+    return out
+
+
+def _qkv_segments():
+    """(first row, rows, kv head) of every per-head row segment of [Wq; Wk; Wv]."""
+
+    segs = []
+    for h in range(NUM_KV_HEADS):
+        segs.append((2 * h * HEAD_DIM, 2 * HEAD_DIM, h))         # q heads 2h, 2h+1
+    for h in range(NUM_KV_HEADS):
+        segs.append((Q_SIZE + h * HEAD_DIM, HEAD_DIM, h))        # k head h
+    for h in range(NUM_KV_HEADS):
+        segs.append((Q_SIZE + KV_SIZE + h * HEAD_DIM, HEAD_DIM, h))  # v head h
+    return segs
+
+
+def build_stages(batch: int, attn_splits: int, num_wgs: int,
+                 num_layers: int = NUM_LAYERS) -> list[Stage]:
+    if batch not in BATCH_BUCKETS:
+        raise ValueError(f"batch bucket must be one of {BATCH_BUCKETS}; got {batch}")
+    if not 1 <= attn_splits <= MAX_SPLITS:
+        raise ValueError(f"attn_splits must be 1..{MAX_SPLITS}; got {attn_splits}")
+    if not 1 <= num_layers <= NUM_LAYERS:
+        raise ValueError(f"num_layers must be 1..{NUM_LAYERS}; got {num_layers}")
+    if num_wgs < 1:
+        raise ValueError("num_wgs must be >= 1")
+    stages: list[Stage] = []
+    qkv_target = -(-QKV_ROWS // num_wgs)
+    prev_down: tuple[int, int] | None = None   # (fanin id, producer count)
+    for layer in range(num_layers):
+        # QKV: per-head segments cut into blocks of ~qkv_target rows
+        qkv = Stage(OP_QKV, layer)
+        per_head = [0] * NUM_KV_HEADS
+        for first, rows, h in _qkv_segments():
+            for r0, n in split_range(first, rows, -(-rows // qkv_target)):
+                wait, cnt = prev_down if prev_down else (-1, 0)
+                qkv.tasks.append(Task(OP_QKV, layer, r0, n, 0, wait, cnt, fanin_qkv(layer, h)))
+                per_head[h] += 1
+        stages.append(qkv)
+        attn = Stage(OP_ATTN, layer)
+        for b in range(batch):
+            for h in range(NUM_KV_HEADS):
+                for s in range(attn_splits):
+                    attn.tasks.append(Task(OP_ATTN, layer, b * NUM_KV_HEADS + h, s, attn_splits,
+                                           fanin_qkv(layer, h), per_head[h], fanin_attn(layer)))
+        stages.append(attn)
+        oproj = Stage(OP_OPROJ, layer)
+        for r0, n in split_range(0, HIDDEN, num_wgs):
+            oproj.tasks.append(Task(OP_OPROJ, layer, r0, n, 0, fanin_attn(layer),
+                                    batch * NUM_KV_HEADS, fanin_oproj(layer)))
+        stages.append(oproj)
+        gu = Stage(OP_GATEUP, layer)
+        for c0, n in split_range(0, INTERMEDIATE, num_wgs):
+            gu.tasks.append(Task(OP_GATEUP, layer, c0, n, 0, fanin_oproj(layer),
+                                 len(oproj.tasks), fanin_gateup(layer)))
+        stages.append(gu)
+        down = Stage(OP_DOWN, layer)
+        for r0, n in split_range(0, HIDDEN, num_wgs):
+            down.tasks.append(Task(OP_DOWN, layer, r0, n, 0, fanin_gateup(layer),
+                                   len(gu.tasks), fanin_down(layer)))
+        stages.append(down)
+        prev_down = (fanin_down(layer), len(down.tasks))
+    lm = Stage(OP_LMHEAD, num_layers)
+    blocks = split_range(0, VOCAB, min(num_wgs, MAX_LM_SLOTS))
+    for slot, (r0, n) in enumerate(blocks):
+        lm.tasks.append(Task(OP_LMHEAD, num_layers, r0, n, slot, prev_down[0], prev_down[1], -1))
+    stages.append(lm)
+    return stages
+
+
+def place_round_robin(stages: list[Stage], num_wgs: int) -> list[list[Task]]:
+    rows: list[list[Task]] = [[] for _ in range(num_wgs)]
+    cursor = 0
+    for st in stages:
+        for t in st.tasks:
+            rows[cursor].append(t)
+            cursor = (cursor + 1) % num_wgs
+    return rows
+
+
+def build_schedule(batch: int, attn_splits: int, num_wgs: int,
+                   num_layers: int = NUM_LAYERS) -> Schedule:
+    stages = build_stages(batch, attn_splits, num_wgs, num_layers)
+    rows = place_round_robin(stages, num_wgs)
+    return Schedule(batch=batch, attn_splits=attn_splits, num_layers=num_layers,
+                    grid=num_wgs, stages=stages, rows=rows)
+
+
+def split_layers(num_layers: int, groups: int) -> list[tuple[int, int]]:
+    """Contiguous layer segments ``[start, end)`` for ``groups`` launches
+    (reference ``schedule.split_layers`` :1168-1195)."""
+
+    if not 1 <= groups <= num_layers:
+        raise ValueError(f"fusion_groups must be in [1, {num_layers}]; got {groups}")
+    return [(r0, r0 + n) for r0, n in split_range(0, num_layers, groups)]
+
+
+def build_segments(batch: int, attn_splits: int, num_wgs: int, num_layers: int = NUM_LAYERS,
+                   groups: int = 1) -> list[Schedule]:
+    """One persistent launch per layer segment. Segment ``k`` holds the stages of
+    its layers (the last one also the LM head); its first QKV stage waits on the
+    previous segment's down counter, which the earlier launch already completed,
+    and the final LM-head task clears every fan-in counter of the step."""
+
+    stages = build_stages(batch, attn_splits, num_wgs, num_layers)
+    out = []
+    for start, end in split_layers(num_layers, groups):
+        seg = [s for s in stages if start <= s.layer < end or (end == num_layers and s.op == OP_LMHEAD)]
+        out.append(Schedule(batch=batch, attn_splits=attn_splits, num_layers=num_layers,
+                            grid=num_wgs, stages=seg, rows=place_round_robin(seg, num_wgs)))
+    return out

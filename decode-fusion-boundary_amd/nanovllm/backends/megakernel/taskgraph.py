@@ -1,0 +1,361 @@
+"""Task-graph decoder: owns the schedules, workspace and per-step staging.
+
+Counterpart of the reference ``backends/megakernel/taskgraph.py``
+(``TaskGraphDecoder`` :147-529, ``taskgraph_compatibility`` :92-131,
+``resolve_num_sms`` :68-83, ``max_pages_per_seq`` :60-65, ``TG_MAX_BATCH`` :35).
+Differences that matter:
+
+* one schedule per (batch bucket 1/2/4/8, split-KV factor); a live batch of 3,
+  5, 6 or 7 runs the next bucket with the extra rows inactive;
+* the split-KV factor follows the context (one split per 256 positions, up to
+  16, never below ``megakernel_attn_splits``);
+* nothing is zeroed per step: the last LM-head task clears the fan-in
+  counters and every ticket counter resets itself (the reference cleared about
+  11.7 MB of scratch per step, ``taskgraph.py:289-295``);
+* ``launch="graph"`` runs the same tasks one kernel per stage from a captured
+  hipGraph (the comparator arm); ``"persistent"`` is one launch per segment.
+
+The step returns after one 128-byte device-to-host read that carries both the
+device error word and the sampled tokens.
+"""
+
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from nanovllm.model_spec import QWEN3_06B
+
+from . import native
+from .row_contract import row_active_mask
+from .schedule import (
+    NUM_LAYERS, Schedule, auto_attn_splits, batch_bucket, build_schedule, build_segments,
+)
+from .verifier import verify
+from .weights import pack_layer_pointers
+
+TG_MAX_BATCH = native.MAX_BATCH
+MAX_ATTN_SPLITS = native.MAX_SPLITS
+
+
+def max_pages_per_seq(max_model_len: int, block_size: int) -> int:
+    if block_size <= 0:
+        raise ValueError("block_size must be positive")
+    return max(1, -(-max_model_len // block_size))
+
+
+def resolve_num_sms(device_cu_count: int) -> int:
+    """Persistent grid: one workgroup per compute unit (``TG_NUM_SMS`` overrides)."""
+
+    override = os.getenv("TG_NUM_SMS")
+    if override:
+        value = int(override)
+        if value <= 0:
+            raise ValueError(f"TG_NUM_SMS must be positive; got {value}")
+        return min(value, int(device_cu_count))
+    return max(1, int(device_cu_count))
+
+
+@dataclass(frozen=True)
+class TaskGraphCompatibility:
+    supported: bool
+    reason: str = ""
+
+
+def taskgraph_compatibility(config: Any, seqs: list[Any], is_prefill: bool) -> TaskGraphCompatibility:
+    """Torch-free admission policy; same rules and reason strings as the reference."""
+
+    if is_prefill:
+        return TaskGraphCompatibility(False, "Task-graph megakernel is decode-only; use the prefill backend")
+    if not seqs:
+        return TaskGraphCompatibility(False, "Task-graph megakernel needs at least one sequence")
+    if len(seqs) > TG_MAX_BATCH:
+        return TaskGraphCompatibility(
+            False,
+            f"Task-graph megakernel supports batch sizes 1..{TG_MAX_BATCH} "
+            "(TG_MAX_BATCH, the compile-time scratch/bar ceiling)",
+        )
+    max_num_seqs = getattr(config, "max_num_seqs", None)
+    if isinstance(max_num_seqs, int) and max_num_seqs < len(seqs):
+        return TaskGraphCompatibility(False, f"batch {len(seqs)} exceeds max_num_seqs={max_num_seqs}")
+    if getattr(config, "tensor_parallel_size", 1) != 1:
+        return TaskGraphCompatibility(False, "Task-graph megakernel requires tensor_parallel_size=1")
+    for seq in seqs:
+        if bool(getattr(seq, "is_greedy", False)):
+            continue
+        temperature = getattr(seq, "temperature", None)
+        if temperature is None or temperature > 1e-10:
+            return TaskGraphCompatibility(False, "Task-graph megakernel supports greedy sampling only")
+    return TaskGraphCompatibility(True)
+
+
+@dataclass
+class _Geometry:
+    batch: int
+    attn_splits: int
+    segments: list[Schedule]
+    persistent: list[tuple[torch.Tensor, torch.Tensor, native.MkdSchedule]]
+    stage_inst: torch.Tensor
+    stages: Any            # ctypes array of MkdStage
+    num_stages: int
+    graph: Any = None      # captured per-op hipGraph (launch="graph")
+
+
+class TaskGraphDecoder:
+    """One greedy decode step of up to 8 rows on the HIP task graph."""
+
+    def __init__(self, weights: dict, *, k_cache, v_cache, block_size: int, num_cache_blocks: int,
+                 max_model_len: int, attn_splits: int = 1, fusion_groups: int = 1,
+                 launch: str = "persistent", verbose: bool = False, debug_bounds: bool = False):
+        self._lib = native.load()
+        if launch not in ("persistent", "graph"):
+            raise ValueError(f"launch must be 'persistent' or 'graph'; got {launch!r}")
+        self.launch = launch
+        self.device = k_cache.device
+        layers = weights["layers"]
+        self.num_layers = len(layers)
+        if self.num_layers > NUM_LAYERS:
+            raise ValueError(f"at most {NUM_LAYERS} layers are compiled; got {self.num_layers}")
+        self._weights = weights
+        self._layer_ptrs = pack_layer_pointers(layers, device=self.device)
+        self._k_cache, self._v_cache = k_cache, v_cache
+        if k_cache.dim() != 5 or k_cache.shape != v_cache.shape or k_cache.dtype != torch.bfloat16:
+            raise ValueError("k_cache/v_cache must be bf16 [layers, blocks, block_size, kv_heads, head_dim]")
+        if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+            raise ValueError("k_cache/v_cache views must be contiguous")
+        self.block_size = int(block_size)
+        self.num_cache_blocks = int(num_cache_blocks)
+        self.max_pages = max_pages_per_seq(int(max_model_len), self.block_size)
+        self.max_model_len = int(max_model_len)
+        if not 1 <= attn_splits <= MAX_ATTN_SPLITS:
+            raise ValueError(f"attn_splits must be 1..{MAX_ATTN_SPLITS}; got {attn_splits}")
+        self.min_attn_splits = int(attn_splits)
+        self.fusion_groups = int(fusion_groups)
+        if not 1 <= self.fusion_groups <= self.num_layers:
+            raise ValueError(f"fusion_groups must be in [1, {self.num_layers}]; got {fusion_groups}")
+        self.verbose = verbose
+        self.debug_bounds = debug_bounds
+
+        cus = native.ctypes.c_int32()
+        lds = native.ctypes.c_int32()
+        dev_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        native.check(self._lib.mkd_device_info(dev_index, native.ctypes.byref(cus), native.ctypes.byref(lds)))
+        self.grid = resolve_num_sms(cus.value)
+
+        i32 = dict(dtype=torch.int32, device=self.device)
+        self._workspace = torch.zeros(int(self._lib.mkd_workspace_bytes()), dtype=torch.uint8, device=self.device)
+        self._status_off = int(self._lib.mkd_status_offset())
+        self._ids = torch.zeros(TG_MAX_BATCH, dtype=torch.int64, device=self.device)
+        self._seqlens = torch.zeros(TG_MAX_BATCH, **i32)
+        self._row_active = torch.ones(TG_MAX_BATCH, **i32)
+        self._mask_dirty = False
+        self._table = torch.zeros(TG_MAX_BATCH, self.max_pages, **i32)
+        self._logits = None
+        self._host_ids = torch.zeros(1, dtype=torch.int64, pin_memory=True)
+        self._host_pos = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self._host_table = torch.zeros(self.max_pages, dtype=torch.int32, pin_memory=True)
+
+        kv_stride = k_cache.stride(0)
+        w = weights
+        self._desc = native.MkdStepDesc(
+            layer_ptrs=self._layer_ptrs.data_ptr(), embed=w["embed"].data_ptr(),
+            final_norm=w["final_norm"].data_ptr(), rope_cos=w["cos"].data_ptr(), rope_sin=w["sin"].data_ptr(),
+            k_cache=k_cache.data_ptr(), v_cache=v_cache.data_ptr(), kv_layer_stride=kv_stride,
+            num_blocks=self.num_cache_blocks, block_size=self.block_size,
+            page_table=self._table.data_ptr(), page_stride=self.max_pages,
+            cache_seqlens=self._seqlens.data_ptr(), row_active=self._row_active.data_ptr(),
+            input_ids=self._ids.data_ptr(),
+            out_tokens=self._workspace.data_ptr() + self._status_off + 64, out_logits=None,
+            workspace=self._workspace.data_ptr(), workspace_bytes=self._workspace.numel(),
+            rows=1, batch=1, num_layers=self.num_layers, lm_slots=1, flags=0,
+        )
+        self._stream_ptr()
+        native.check(self._lib.mkd_reset_counters(native.ctypes.byref(self._desc), self._stream_ptr()))
+        self._geometries: dict[tuple[int, int], _Geometry] = {}
+        for b in (1, 2, 4, 8):
+            self._geometry(b, self.min_attn_splits)
+        if verbose:
+            g = self._geometries[(1, self.min_attn_splits)]
+            print(f"taskgraph decoder: grid={self.grid} launch={self.launch} layers={self.num_layers} "
+                  f"fusion_groups={self.fusion_groups} max_pages={self.max_pages} "
+                  f"tasks(B=1)={sum(s.num_tasks for s in g.segments)}")
+
+    # -- helpers -------------------------------------------------------------
+    def _stream_ptr(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _geometry(self, batch: int, splits: int) -> _Geometry:
+        key = (batch, splits)
+        geo = self._geometries.get(key)
+        if geo is not None:
+            return geo
+        segs = build_segments(batch, splits, self.grid, self.num_layers, self.fusion_groups)
+        whole = build_schedule(batch, splits, self.grid, self.num_layers)
+        errors = verify(whole)
+        if errors:
+            raise RuntimeError("task-graph schedule failed verification: " + "; ".join(errors[:3]))
+        persistent = []
+        for seg in segs:
+            flat, counts = seg.persistent_words()
+            inst = torch.tensor(flat, dtype=torch.int32).to(self.device)
+            num = torch.tensor(counts, dtype=torch.int32).to(self.device)
+            sched = native.MkdSchedule(inst=inst.data_ptr(), num_inst=num.data_ptr(), grid=seg.grid,
+                                       max_inst=seg.max_inst)
+            persistent.append((inst, num, sched))
+        flat, table = whole.stage_words()
+        stage_inst = torch.tensor(flat, dtype=torch.int32).to(self.device)
+        stages = (native.MkdStage * len(table))(*[native.MkdStage(*row) for row in table])
+        geo = _Geometry(batch=batch, attn_splits=splits, segments=segs, persistent=persistent,
+                        stage_inst=stage_inst, stages=stages, num_stages=len(table))
+        self._geometries[key] = geo
+        return geo
+
+    def _desc_for(self, rows: int, geo: _Geometry, flags: int = 0, logits=None) -> native.MkdStepDesc:
+        d = native.MkdStepDesc.from_buffer_copy(self._desc)
+        d.rows = rows
+        d.batch = geo.batch
+        d.lm_slots = geo.segments[-1].lm_slots
+        d.flags = flags
+        d.out_logits = None if logits is None else logits.data_ptr()
+        return d
+
+    def _launch(self, desc: native.MkdStepDesc, geo: _Geometry, mode: str | None = None) -> None:
+        stream = self._stream_ptr()
+        mode = mode or self.launch
+        if mode == "persistent":
+            for _, _, sched in geo.persistent:
+                native.check(self._lib.mkd_launch_persistent(native.ctypes.byref(desc),
+                                                             native.ctypes.byref(sched), stream))
+        elif mode == "stages":
+            native.check(self._lib.mkd_launch_stages(native.ctypes.byref(desc), geo.stage_inst.data_ptr(),
+                                                     geo.stages, geo.num_stages, stream))
+        else:  # graph
+            if geo.graph is None or geo.graph[0] != (desc.rows, desc.flags, desc.out_logits):
+                if geo.graph is not None:
+                    self._lib.mkd_graph_destroy(geo.graph[1])
+                handle = native.ctypes.c_void_p()
+                native.check(self._lib.mkd_graph_create(
+                    native.ctypes.byref(desc), 0, None, geo.stage_inst.data_ptr(), geo.stages,
+                    geo.num_stages, 1, stream, native.ctypes.byref(handle)))
+                geo.graph = ((desc.rows, desc.flags, desc.out_logits), handle)
+            native.check(self._lib.mkd_graph_launch(geo.graph[1], stream))
+
+    def _read_status(self, rows: int) -> list[int]:
+        status = self._workspace[self._status_off:self._status_off + 128].view(torch.int32).cpu()
+        err = int(status[0])
+        if err != 0:
+            native.check(self._lib.mkd_reset_counters(native.ctypes.byref(self._desc), self._stream_ptr()))
+            torch.cuda.synchronize(self.device)
+            kind = {1: "a dependency wait timed out", 2: "a stage kernel met a foreign instruction",
+                    3: "a position, block id or token id was out of range"}.get(err, "unknown")
+            raise native.MegakernelError(f"decode step failed on the device (error {err}: {kind})")
+        return status[16:16 + rows].tolist()
+
+    def splits_for(self, max_context: int) -> int:
+        return auto_attn_splits(max_context, self.min_attn_splits)
+
+    # -- decode ----------------------------------------------------------------
+    def decode_rows(self, input_ids, positions, block_tables, active_rows=None, logits=None,
+                    mode: str | None = None) -> list[int]:
+        """One step for every row. ``input_ids``/``positions``: int64 device ``[rows]``
+        (positions = pre-decode length); ``block_tables``: int32 device ``[rows, cols]``
+        padded with 0. ``logits`` (optional bf16 ``[rows, vocab]``) receives the logits."""
+
+        rows = int(input_ids.numel())
+        if rows == 0:
+            return []
+        if rows > TG_MAX_BATCH:
+            raise RuntimeError(
+                f"decode_rows got {rows} rows but this decoder is sized for {TG_MAX_BATCH} (TG_MAX_BATCH); "
+                "the backend's compatibility check should have rejected this batch upstream")
+        cols = int(block_tables.size(1))
+        if cols > self.max_pages:
+            raise ValueError(
+                f"block table has {cols} columns but the task-graph page_table stride is "
+                f"{self.max_pages} (max_model_len // block_size)")
+        geo = self._geometry(batch_bucket(rows), self.splits_for(cols * self.block_size))
+        self._ids[:rows].copy_(input_ids)
+        self._seqlens[:rows].copy_(positions)
+        self._table[:rows, :cols].copy_(block_tables)
+        if active_rows is not None:
+            mask = row_active_mask(active_rows, rows)
+            self._row_active[:rows].copy_(torch.tensor(mask, dtype=torch.int32))
+            self._mask_dirty = True
+        elif self._mask_dirty:
+            self._row_active.fill_(1)
+            self._mask_dirty = False
+        self._launch(self._desc_for(rows, geo, logits=logits), geo, mode)
+        return self._read_status(rows)
+
+    def decode_row(self, token_id: int, position: int, block_table) -> int:
+        """Batch-1 step from host values (pinned staging, no per-step allocation)."""
+
+        table = block_table.tolist() if torch.is_tensor(block_table) else list(block_table)
+        cols = min(len(table), self.max_pages)
+        if len(table) > self.max_pages:
+            raise ValueError(f"block table has {len(table)} pages but the stride is {self.max_pages}")
+        self._host_ids[0] = int(token_id)
+        self._host_pos[0] = int(position)
+        self._host_table[:cols] = torch.as_tensor(table[:cols], dtype=torch.int32)
+        self._ids[:1].copy_(self._host_ids, non_blocking=True)
+        self._seqlens[:1].copy_(self._host_pos, non_blocking=True)
+        self._table[0, :cols].copy_(self._host_table[:cols], non_blocking=True)
+        if self._mask_dirty:
+            self._row_active.fill_(1)
+            self._mask_dirty = False
+        geo = self._geometry(1, self.splits_for(cols * self.block_size))
+        self._launch(self._desc_for(1, geo), geo)
+        return int(self._read_status(1)[0])
+
+    def step(self, token_id: int, position: int | None = None, block_table=None) -> int:
+        if position is None or block_table is None:
+            raise ValueError("task-graph decode requires position and block_table")
+        return self.decode_row(token_id, position, block_table)
+
+    def step_batch(self, input_token_ids, positions, block_tables) -> list[int]:
+        return self.decode_rows(input_token_ids, positions, block_tables)
+
+    # -- device-resident loop (benchmarks) --------------------------------------
+    def stage_rows(self, input_ids, positions, block_tables) -> None:
+        """Load a batch into the decoder's own buffers for :meth:`run_steps`."""
+
+        rows = int(input_ids.numel())
+        cols = int(block_tables.size(1))
+        self._ids[:rows].copy_(input_ids)
+        self._seqlens[:rows].copy_(positions)
+        self._table[:rows, :cols].copy_(block_tables)
+        self._row_active.fill_(1)
+        self._mask_dirty = False
+
+    def prepare_steps(self, rows: int, max_context: int, mode: str = "persistent"):
+        """Return a zero-argument callable that runs one device-resident step
+        (token fed back, position advanced on the device, no host sync)."""
+
+        geo = self._geometry(batch_bucket(rows), self.splits_for(max_context))
+        desc = self._desc_for(rows, geo, flags=native.FLAG_ADVANCE)
+        if mode == "graph":
+            handle = native.ctypes.c_void_p()
+            native.check(self._lib.mkd_graph_create(
+                native.ctypes.byref(desc), 0, None, geo.stage_inst.data_ptr(), geo.stages,
+                geo.num_stages, 1, self._stream_ptr(), native.ctypes.byref(handle)))
+            self._owned_graphs = getattr(self, "_owned_graphs", []) + [handle]
+            return lambda: native.check(self._lib.mkd_graph_launch(handle, self._stream_ptr()))
+        return lambda: self._launch(desc, geo, mode)
+
+    def check_device_error(self) -> None:
+        self._read_status(0)
+
+    def tokens(self, rows: int) -> list[int]:
+        return self._read_status(rows)
+
+    def close(self) -> None:
+        for geo in self._geometries.values():
+            if geo.graph is not None:
+                self._lib.mkd_graph_destroy(geo.graph[1])
+                geo.graph = None
+        for h in getattr(self, "_owned_graphs", []):
+            self._lib.mkd_graph_destroy(h)
+        self._owned_graphs = []
