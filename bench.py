@@ -130,7 +130,7 @@ def main():
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--mode", default="persistent", choices=["persistent", "graph"])
+    ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "stages"])
     ap.add_argument("--only-kernel", action="store_true", help="timed loop only (for profilers)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -106,15 +106,31 @@ __device__ __forceinline__ uint32_t add_co(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ void drain() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ---- wave reductions (wave64) --------------------------------------------------
+// DPP butterfly: quad swaps, row half-mirror and mirror give every lane its
+// 16-lane row total; row_bcast15 / row_bcast31 fold the four rows into lane
+// 63, which is read back as a uniform value. Six VALU DPP ops instead of six
+// LDS-crossbar (ds_bpermute) round trips.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_mov(float v, float old) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_mov<0xB1>(v, 0.f);         // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v, 0.f);         // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v, 0.f);        // row_half_mirror
+  v += dpp_mov<0x140>(v, 0.f);        // row_mirror
+  v += dpp_mov<0x142, 0xA>(v, 0.f);   // row_bcast15 -> rows 1, 3
+  v += dpp_mov<0x143, 0xC>(v, 0.f);   // row_bcast31 -> rows 2, 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_mov<0xB1>(v, -INFINITY));
+  v = fmaxf(v, dpp_mov<0x4E>(v, -INFINITY));
+  v = fmaxf(v, dpp_mov<0x141>(v, -INFINITY));
+  v = fmaxf(v, dpp_mov<0x140>(v, -INFINITY));
+  v = fmaxf(v, dpp_mov<0x142, 0xA>(v, -INFINITY));
+  v = fmaxf(v, dpp_mov<0x143, 0xC>(v, -INFINITY));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // ---- workspace views -----------------------------------------------------------

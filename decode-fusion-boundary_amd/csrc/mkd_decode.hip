@@ -16,7 +16,7 @@
 #include <string>
 #include <vector>
 
-#include "mkd_tasks.h"
+#include "mkd_persistent.h"
 
 using namespace mkd;
 
@@ -140,6 +140,8 @@ int validate(const MkdStepDesc* d) {
     return fail(MKD_E_INVALID, "workspace missing or smaller than mkd_workspace_bytes()");
   if (d->block_size < 1 || d->num_blocks < 1 || d->page_stride < 1)
     return fail(MKD_E_INVALID, "invalid paged-KV geometry");
+  if ((MKD_MAX_POSITION + d->block_size - 1) / d->block_size > MAX_PAGES)
+    return fail(MKD_E_INVALID, "block_size too small: a 2048-token context needs more than 64 blocks");
   const void* ptrs[] = {d->layer_ptrs, d->embed, d->final_norm, d->rope_cos, d->rope_sin, d->k_cache,
                         d->v_cache, d->page_table, d->cache_seqlens, d->row_active, d->input_ids, d->out_tokens};
   for (const void* p : ptrs)
@@ -149,7 +151,17 @@ int validate(const MkdStepDesc* d) {
 
 template <int B>
 int launch_persistent_b(const MkdStepDesc& d, const MkdSchedule& s, hipStream_t st) {
-  hipLaunchKernelGGL(k_persistent<B>, dim3(s.grid), dim3(NT), 0, st, d, s);
+  if (d.flags & MKD_FLAG_PK_V1) {
+    hipLaunchKernelGGL(k_persistent<B>, dim3(s.grid), dim3(NT), 0, st, d, s);
+  } else {
+    static bool attr_set = false;  // per instantiation; set before the first launch
+    if (!attr_set) {
+      MKD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_persistent2<B>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, PkCfg<B>::LDS_BYTES));
+      attr_set = true;
+    }
+    hipLaunchKernelGGL(k_persistent2<B>, dim3(s.grid), dim3(PK_THREADS), PkCfg<B>::LDS_BYTES, st, d, s);
+  }
   MKD_HIP(hipGetLastError());
   return MKD_OK;
 }

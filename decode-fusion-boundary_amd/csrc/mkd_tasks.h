@@ -13,7 +13,13 @@
 namespace mkd {
 
 constexpr int SMEM_BYTES = MAXB * I * 2 + 4096;  // activation tile + reduction scratch
+
+// Workgroup-wide barrier (per-op kernels: every thread runs the task).
+struct SyncAll {
+  __device__ __forceinline__ void operator()() const { __syncthreads(); }
+};
 constexpr float ATTN_SCALE = 0.08838834764831845f;  // 128 ** -0.5
+constexpr int MAX_PAGES = 64;  // block-table entries staged per attention task (>= 2048 / block_size)
 
 __device__ __forceinline__ const uint16_t* wptr(const MkdStepDesc& d, int layer, int which) {
   return reinterpret_cast<const uint16_t*>(d.layer_ptrs[layer * MKD_LAYER_PTRS + which]);
@@ -26,10 +32,10 @@ __device__ __forceinline__ const uint16_t* wptr(const MkdStepDesc& d, int layer,
 // s = hidden + residual in fp32; xs = bf16(bf16(s * rsqrt(mean(s^2)+eps)) * w);
 // when write_resid, the new residual bf16(s) goes to resid(norm_idx + 1).
 // ---------------------------------------------------------------------------
-template <int B>
+template <int B, class Sync = SyncAll>
 __device__ void stage_norm(const MkdStepDesc& d, const Ws& ws, int norm_idx,
                            const uint16_t* hidden, const uint16_t* w, uint16_t* xs,
-                           float* red, bool write_resid) {
+                           float* red, bool write_resid, Sync sync = Sync()) {
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const int k0 = t * 4;  // 4 consecutive features per thread
   float s[B][4];
@@ -71,7 +77,7 @@ __device__ void stage_norm(const MkdStepDesc& d, const Ws& ws, int norm_idx,
     ss = wave_sum(ss);
     if (lane == 0) red[wave * MAXB + b] = ss;
   }
-  __syncthreads();
+  sync();
   const uint2 wv = *reinterpret_cast<const uint2*>(w + k0);
   const float w4[4] = {bf_lo(wv.x), bf_hi(wv.x), bf_lo(wv.y), bf_hi(wv.y)};
 #pragma unroll
@@ -83,19 +89,19 @@ __device__ void stage_norm(const MkdStepDesc& d, const Ws& ws, int norm_idx,
     for (int j = 0; j < 4; j++) o[j] = f2bf(round_bf(s[b][j] * r) * w4[j]);
     *reinterpret_cast<uint2*>(xs + (size_t)b * H + k0) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
   }
-  __syncthreads();
+  sync();
 }
 
 // Copy B rows of a bf16 activation [B][K] (row stride ld) from global into LDS.
-template <int B, int K>
-__device__ void stage_copy(const uint16_t* src, int ld, uint16_t* xs) {
+template <int B, int K, class Sync = SyncAll>
+__device__ void stage_copy(const uint16_t* src, int ld, uint16_t* xs, Sync sync = Sync()) {
   constexpr int PER_ROW = K / 4;  // 64-bit words per row
   for (int i = threadIdx.x; i < B * PER_ROW; i += NT) {
     const int b = i / PER_ROW, c = i % PER_ROW;
     reinterpret_cast<uint64_t*>(xs + (size_t)b * K)[c] =
         ld_co(reinterpret_cast<const uint64_t*>(src + (size_t)b * ld) + c);
   }
-  __syncthreads();
+  sync();
 }
 
 // ---------------------------------------------------------------------------
@@ -215,9 +221,9 @@ __device__ void task_gateup(const MkdStepDesc& d, const Ws& ws, int layer, int c
 // positions; splits are merged by the last arriving split (ticket counter).
 // Returns true when this workgroup produced the final attention output.
 // ---------------------------------------------------------------------------
-template <int B>
-__device__ bool task_attn(const MkdStepDesc& d, const Ws& ws, int layer, int bh, int split, int nsplit,
-                          uint8_t* smem) {
+template <int B, class Sync = SyncAll>
+__device__ __forceinline__ bool task_attn(const MkdStepDesc& d, const Ws& ws, int layer, int bh, int split, int nsplit,
+                          uint8_t* smem, Sync sync = Sync()) {
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const int b = bh / NKV, h = bh % NKV;
   bool live = b < d.rows;
@@ -239,9 +245,14 @@ __device__ bool task_attn(const MkdStepDesc& d, const Ws& ws, int layer, int bh,
   float* mrg = reinterpret_cast<float*>(smem + 1024);        // [4 waves][2][128] + m/l
   float* mrg_ml = mrg + NWAVE * GROUP * HD;                  // [4][2] m, [4][2] l
   int* sh = reinterpret_cast<int*>(mrg_ml + 2 * NWAVE * GROUP);
+  int* pages = sh + 4;                                       // [MAX_PAGES] this row's physical blocks
 
-  // -- q/k norm + RoPE (waves 0,1: q heads 2h, 2h+1; wave 2: k; wave 3: v copy)
+  // -- the row's block table (clamped to the cache) into LDS; q/k norm + RoPE
+  //    (waves 0,1: q heads 2h, 2h+1; wave 2: k; wave 3: v copy)
   {
+    const int n_pages = live ? min(pos / d.block_size + 1, MAX_PAGES) : 0;
+    for (int i = t; i < n_pages; i += NT)
+      pages[i] = min(max(d.page_table[(size_t)b * d.page_stride + i], 0), d.num_blocks - 1);
     const uint16_t* row = ws.qkv() + (size_t)b * QKV_N;
     const uint16_t* src = wave < 2 ? row + (GROUP * h + wave) * HD : (wave == 2 ? row + QS + h * HD : row + QS + KVS + h * HD);
     const float x0 = bf2f(ld_co(src + lane)), x1 = bf2f(ld_co(src + lane + 64));
@@ -260,7 +271,7 @@ __device__ bool task_attn(const MkdStepDesc& d, const Ws& ws, int layer, int bh,
       dst[lane + 64] = (uint16_t)f2bf(x1);
     }
   }
-  __syncthreads();
+  sync();
   const int32_t* table = d.page_table + (size_t)b * d.page_stride;
   const size_t layer_off = (size_t)layer * (size_t)d.kv_layer_stride + (size_t)h * HD;
   if (split == 0 && active && t < 128) {
@@ -289,21 +300,34 @@ __device__ bool task_attn(const MkdStepDesc& d, const Ws& ws, int layer, int bh,
 
   // Cached positions [p_begin, c_end): everything before this token's own
   // position. The token itself (pos) is attended from LDS below, so the
-  // loop never depends on this step's cache write.
+  // loop never depends on this step's cache write. Per 64-position tile a
+  // lane loads one K row (scores: one position per lane) and, for P*V, the
+  // 16 V slices of positions t0 + 4*it + sub (dims dg..dg+8); all 32 loads
+  // are issued before any math so the tile costs one memory round trip.
   const int c_end = min(p_end, pos);
   const int dg = (lane & 15) * 8, sub = lane >> 4;
+  const uint16_t* kbase = d.k_cache + layer_off;
+  const uint16_t* vbase = d.v_cache + layer_off;
   for (int t0 = p_begin + wave * 64; t0 < c_end; t0 += NWAVE * 64) {
-    // scores: one position per lane
+    asm volatile("" ::: "memory");  // keep the q reads (LDS) inside the tile: hoisting them costs 128 VGPRs
     const int p = t0 + lane;
     const bool valid = p < c_end;
     const int pc = valid ? p : t0;
-    const uint4* krow = reinterpret_cast<const uint4*>(d.k_cache + layer_off + ((size_t)min(max(table[pc / bs], 0), nblk - 1) * bs + pc % bs) * KVS);
+    const uint4* krow = reinterpret_cast<const uint4*>(kbase + ((size_t)pages[pc / bs] * bs + pc % bs) * KVS);
+    uint4 kreg[HD / 8], vreg[16];
+#pragma unroll
+    for (int i = 0; i < HD / 8; i++) kreg[i] = krow[i];
+#pragma unroll
+    for (int it = 0; it < 16; it++) {
+      int pp = t0 + 4 * it + sub;
+      pp = pp < c_end ? pp : t0;
+      vreg[it] = *reinterpret_cast<const uint4*>(vbase + ((size_t)pages[pp / bs] * bs + pp % bs) * KVS + dg);
+    }
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
     for (int i = 0; i < HD / 8; i++) {
-      const uint4 k = krow[i];
-      s0 = dot8(k, q0[i], s0);
-      s1 = dot8(k, q1[i], s1);
+      s0 = dot8(kreg[i], q0[i], s0);
+      s1 = dot8(kreg[i], q1[i], s1);
     }
     s0 = valid ? s0 * ATTN_SCALE : -INFINITY;
     s1 = valid ? s1 * ATTN_SCALE : -INFINITY;
@@ -315,17 +339,13 @@ __device__ bool task_attn(const MkdStepDesc& d, const Ws& ws, int layer, int bh,
     m0 = n0; m1 = n1;
 #pragma unroll
     for (int j = 0; j < 8; j++) { a0[j] *= al0; a1[j] *= al1; }
-    // P*V: lane owns dims dg..dg+8 of positions t0 + 4*it + sub
-#pragma unroll 4
-    for (int it = 0; it < 16; it++) {
-      const int pp = t0 + 4 * it + sub;
-      const float w0 = __shfl(p0, 4 * it + sub, 64), w1 = __shfl(p1, 4 * it + sub, 64);
-      if (pp < c_end) {
-        const uint4 v = *reinterpret_cast<const uint4*>(d.v_cache + layer_off + ((size_t)min(max(table[pp / bs], 0), nblk - 1) * bs + pp % bs) * KVS + dg);
-        const float vf[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
 #pragma unroll
-        for (int j = 0; j < 8; j++) { a0[j] += w0 * vf[j]; a1[j] += w1 * vf[j]; }
-      }
+    for (int it = 0; it < 16; it++) {
+      const float w0 = __shfl(p0, 4 * it + sub, 64), w1 = __shfl(p1, 4 * it + sub, 64);  // 0 past c_end
+      const uint4 v = vreg[it];
+      const float vf[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
+#pragma unroll
+      for (int j = 0; j < 8; j++) { a0[j] += w0 * vf[j]; a1[j] += w1 * vf[j]; }
     }
   }
   // The token's own K/V (position pos) belongs to the split whose range holds it.
@@ -364,7 +384,7 @@ __device__ bool task_attn(const MkdStepDesc& d, const Ws& ws, int layer, int bh,
     mrg_ml[wave * GROUP + 0] = m0; mrg_ml[wave * GROUP + 1] = m1;
     mrg_ml[NWAVE * GROUP + wave * GROUP + 0] = l0; mrg_ml[NWAVE * GROUP + wave * GROUP + 1] = l1;
   }
-  __syncthreads();
+  sync();
   const int g = t >> 7, dd = t & 127;  // 256 threads = 2 heads x 128 dims
   float M = -INFINITY;
 #pragma unroll
@@ -387,7 +407,7 @@ __device__ bool task_attn(const MkdStepDesc& d, const Ws& ws, int layer, int bh,
   st_co(part + g * HD + dd, num);
   if (dd == 0) { st_co(part + GROUP * HD + g, M); st_co(part + GROUP * HD + GROUP + g, den); }
   drain();
-  __syncthreads();
+  sync();
   if (t == 0) {
     uint32_t* ticket = ws.line(CTR_COMB_BASE + (layer * MAXB + b) * NKV + h);
     const uint32_t old = add_co(ticket, 1u);
@@ -395,7 +415,7 @@ __device__ bool task_attn(const MkdStepDesc& d, const Ws& ws, int layer, int bh,
     if (last) st_co(ticket, 0u);
     sh[0] = last;
   }
-  __syncthreads();
+  sync();
   if (!sh[0]) return false;
   float Ms = -INFINITY;
   for (int s = 0; s < nsplit; s++) Ms = fmaxf(Ms, ld_co(ws.apart(b, h, s) + GROUP * HD + g));

@@ -66,6 +66,7 @@ class MkdStepDesc(ctypes.Structure):
         ("lm_slots", ctypes.c_int32),
         ("flags", ctypes.c_uint32),
         ("_pad1", ctypes.c_int32),
+        ("trace", ctypes.c_void_p),
     ]
 
 

@@ -86,6 +86,7 @@ enum MkdInstWord {
 
 #define MKD_FLAG_ADVANCE 1u   /* after the step: input_ids[b] = token, cache_seqlens[b] += 1 */
 #define MKD_FLAG_ZERO_FANIN 2u /* set by the persistent launch: last LM task clears fan-in counters */
+#define MKD_FLAG_PK_V1 4u      /* persistent launch without LDS-DMA weight streaming (A/B reference) */
 
 typedef struct MkdStepDesc {
   /* weights (device) */
@@ -119,6 +120,10 @@ typedef struct MkdStepDesc {
   int32_t lm_slots;             /* number of LMHEAD tasks (argmax partial slots) */
   uint32_t flags;               /* MKD_FLAG_* */
   int32_t _pad1;
+  /* optional [grid][max_inst][4] uint64 timestamps (100 MHz device clock) of
+   * the persistent kernel's tasks: start, dependency met, inputs staged, done;
+   * NULL to skip (diagnostics only) */
+  uint64_t* trace;
 } MkdStepDesc;
 
 /* A task list uploaded to the device. For mkd_launch_persistent it is
