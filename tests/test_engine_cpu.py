@@ -1,0 +1,147 @@
+"""Plugin surface on the CPU: admission (reference reason strings), the Qwen3
+contract, config validation, the runner's fallback reporting, and the
+engine end to end on the torch path."""
+
+from __future__ import annotations
+
+import os
+import warnings
+from types import SimpleNamespace
+
+import pytest
+
+from conftest import ROOT
+from nanovllm.backends.megakernel import (
+    MegakernelBackend, TG_MAX_BATCH, gcn_arch_supported, qwen3_contract_mismatch, taskgraph_compatibility,
+)
+from nanovllm.backends.megakernel.row_contract import row_active_mask
+
+
+def _cfg(**kw):
+    hf = SimpleNamespace(tie_word_embeddings=True, attention_bias=False, model_type="qwen3", hidden_size=1024,
+                         intermediate_size=3072, num_hidden_layers=28, num_attention_heads=16,
+                         num_key_value_heads=8, vocab_size=151936, head_dim=128)
+    for k, v in kw.pop("hf", {}).items():
+        setattr(hf, k, v)
+    base = dict(hf_config=hf, max_num_seqs=8, tensor_parallel_size=1, max_model_len=2048)
+    base.update(kw)
+    return SimpleNamespace(**base)
+
+
+def _seq(t=0.0):
+    return SimpleNamespace(temperature=t, is_greedy=t <= 1e-10)
+
+
+def test_admission_reasons():
+    cfg = _cfg()
+    assert taskgraph_compatibility(cfg, [_seq()], True).reason == \
+        "Task-graph megakernel is decode-only; use the prefill backend"
+    assert taskgraph_compatibility(cfg, [], False).reason == "Task-graph megakernel needs at least one sequence"
+    assert "batch sizes 1..8" in taskgraph_compatibility(cfg, [_seq()] * 9, False).reason
+    assert taskgraph_compatibility(_cfg(max_num_seqs=2), [_seq()] * 3, False).reason == \
+        "batch 3 exceeds max_num_seqs=2"
+    assert taskgraph_compatibility(_cfg(tensor_parallel_size=2), [_seq()], False).reason == \
+        "Task-graph megakernel requires tensor_parallel_size=1"
+    assert taskgraph_compatibility(cfg, [_seq(0.7)], False).reason == \
+        "Task-graph megakernel supports greedy sampling only"
+    for n in range(1, TG_MAX_BATCH + 1):
+        assert taskgraph_compatibility(cfg, [_seq()] * n, False).supported
+
+
+def test_qwen3_contract():
+    assert qwen3_contract_mismatch(_cfg()) is None
+    assert qwen3_contract_mismatch(_cfg(hf={"tie_word_embeddings": False})) == "tie_word_embeddings"
+    assert qwen3_contract_mismatch(_cfg(hf={"attention_bias": True})) == "attention_bias"
+    assert qwen3_contract_mismatch(_cfg(hf={"num_hidden_layers": 2})) == "num_hidden_layers"
+    assert qwen3_contract_mismatch(_cfg(max_model_len=4096)) == "max_model_len"
+    assert MegakernelBackend.compatibility(_cfg(hf={"vocab_size": 1000}), [_seq()], False).reason == \
+        "unsupported Qwen config: vocab_size"
+
+
+def test_backend_surface_without_gpu():
+    be = MegakernelBackend(_cfg(), model=None)
+    with pytest.raises(ValueError, match="kv_cache must have shape"):
+        be.set_kv_cache(None)
+    assert not be.ready
+    be.disable("manual")
+    with pytest.raises(RuntimeError, match="manual"):
+        be.ensure_ready()
+    assert gcn_arch_supported("gfx950:sramecc+:xnack-") and not gcn_arch_supported("gfx942")
+
+
+def test_row_active_mask():
+    assert row_active_mask(None, 3) == [1, 1, 1]
+    assert row_active_mask([True, 0, 5], 3) == [1, 0, 1]
+    with pytest.raises(ValueError):
+        row_active_mask([1], 2)
+    with pytest.raises(ValueError):
+        row_active_mask([0, 0], 2)
+
+
+def test_config_validation(tmp_path):
+    from nanovllm.config import Config
+    from nanovllm.synthetic import write_model_dir
+
+    path = write_model_dir(str(tmp_path), num_layers=1)
+    with pytest.raises(ValueError, match="decode_backend"):
+        Config(path, decode_backend="cuda")
+    with pytest.raises(ValueError, match="multiple of 256"):
+        Config(path, kvcache_block_size=128)
+    with pytest.raises(ValueError, match="megakernel_launch"):
+        Config(path, megakernel_launch="eager")
+    with pytest.raises(ValueError, match="does not exist"):
+        Config(str(tmp_path / "missing"))
+    cfg = Config(path, max_model_len=1 << 20)
+    assert cfg.max_model_len == 40960 and cfg.hf_config.num_hidden_layers == 1
+
+
+def test_engine_megakernel_falls_back_with_reason_on_cpu():
+    """No GPU here: the backend is disabled at startup with an explicit reason,
+    and every decode step reports the torch path plus that reason."""
+    from nanovllm import LLM, SamplingParams
+    from nanovllm.synthetic import write_model_dir
+
+    path = write_model_dir(os.path.join(ROOT, "_work", "test_model_2l"), num_layers=2)
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        llm = LLM(path, max_model_len=2048, num_kvcache_blocks=4, decode_backend="megakernel")
+    assert any("Megakernel disabled at startup" in str(w.message) for w in caught)
+    res = llm.generate_with_metrics([[5, 6, 7]], SamplingParams(temperature=0.0, max_tokens=3, ignore_eos=True))
+    m = res["metrics"]
+    assert m["decode_backends"] == {"torch": 2}
+    assert list(m["fallback_reasons"]) == ["Megakernel requires a ROCm (HIP) device"]
+    assert len(res["outputs"][0]["token_ids"]) == 3
+
+
+def test_engine_megakernel_warns_on_long_max_model_len():
+    from nanovllm import LLM
+    from nanovllm.synthetic import write_model_dir
+
+    path = write_model_dir(os.path.join(ROOT, "_work", "test_model_2l"), num_layers=2)
+    with pytest.warns(RuntimeWarning, match="requires max_model_len <= 2048"):
+        LLM(path, max_model_len=4096, num_kvcache_blocks=4, decode_backend="megakernel")
+
+
+def test_scheduler_batches_and_preempts(tmp_path):
+    from nanovllm import SamplingParams
+    from nanovllm.config import Config
+    from nanovllm.engine.scheduler import Scheduler
+    from nanovllm.engine.sequence import Sequence
+    from nanovllm.synthetic import write_model_dir
+
+    Sequence.block_size = 256
+    cfg = Config(write_model_dir(str(tmp_path), num_layers=1), num_kvcache_blocks=3, max_num_seqs=4)
+    sched = Scheduler(cfg)
+    seqs = [Sequence([1] * 200, SamplingParams(max_tokens=100)) for _ in range(3)]
+    for s in seqs:
+        sched.add(s)
+    picked, prefill = sched.schedule()
+    assert prefill and len(picked) == 3
+    sched.postprocess(picked, [9, 9, 9], True)
+    for _ in range(60):   # grow until the pool is exhausted: someone must be preempted
+        picked, prefill = sched.schedule()
+        if prefill:
+            break
+        sched.postprocess(picked, [9] * len(picked), False)
+    assert sched.block_manager.stats()["allocated_blocks"] <= 3
+    assert any(s.status.name == "WAITING" for s in seqs) or prefill

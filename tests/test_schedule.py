@@ -1,0 +1,99 @@
+"""Task-graph generator + verifier (CPU): every supported geometry verifies
+(deadlock-free by maximal execution, exact arrivals, single ownership), and
+the verifier rejects mutated schedules."""
+
+from __future__ import annotations
+
+import copy
+import dataclasses
+
+import pytest
+
+from nanovllm.backends.megakernel import native
+from nanovllm.backends.megakernel.schedule import (
+    Task, auto_attn_splits, batch_bucket, build_schedule, build_segments, split_layers,
+)
+from nanovllm.backends.megakernel.verifier import arrivals, ownership, simulate, verify
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
+@pytest.mark.parametrize("grid", [1, 7, 64, 256])
+@pytest.mark.parametrize("splits", [1, 4, 16])
+def test_geometries_verify(batch, grid, splits):
+    layers = 2 if grid < 64 else 28
+    sched = build_schedule(batch, splits, grid, layers)
+    assert verify(sched) == []
+
+
+def test_segments_cover_the_step_and_verify_jointly():
+    whole = build_schedule(2, 2, 256, 28)
+    segs = build_segments(2, 2, 256, 28, groups=4)
+    assert sum(s.num_tasks for s in segs) == whole.num_tasks
+    assert split_layers(28, 4) == [(0, 7), (7, 14), (14, 21), (21, 28)]
+    # running the segments back to back is the whole schedule run in order
+    merged = dataclasses.replace(whole, rows=[sum((s.rows[g] for s in segs), []) for g in range(256)])
+    assert simulate(merged) == []
+
+
+def test_task_counts_at_256_cus():
+    s = build_schedule(1, 1, 256, 28)
+    by_op = {}
+    for st in s.stages:
+        by_op.setdefault(st.op, []).append(len(st.tasks))
+    assert by_op[native.OP_QKV][0] == 256 and by_op[native.OP_OPROJ][0] == 256
+    assert by_op[native.OP_GATEUP][0] == 256 and by_op[native.OP_DOWN][0] == 256
+    assert by_op[native.OP_ATTN][0] == 8 and by_op[native.OP_LMHEAD] == [256]
+    assert s.lm_slots == 256
+
+
+def _mutate(sched, fn):
+    m = copy.deepcopy(sched)
+    fn(m)
+    return m
+
+
+def test_verifier_rejects_mutants():
+    base = build_schedule(1, 2, 16, 2)
+    assert verify(base) == []
+
+    def wrong_count(m):
+        t = m.stages[2].tasks[0]
+        m.stages[2].tasks[0] = dataclasses.replace(t, wait_count=t.wait_count + 1)
+        m.rows = [[m.stages[2].tasks[0] if x is t else x for x in r] for r in m.rows]
+
+    def reversed_row(m):
+        m.rows[0] = list(reversed(m.rows[0]))
+
+    def duplicate_row(m):
+        t = m.stages[0].tasks[1]
+        m.stages[0].tasks[1] = dataclasses.replace(t, a0=m.stages[0].tasks[0].a0)
+
+    def missing_signal(m):
+        t = m.stages[4].tasks[0]
+        new = dataclasses.replace(t, signal=-1)
+        m.stages[4].tasks[0] = new
+        m.rows = [[new if x is t else x for x in r] for r in m.rows]
+
+    assert arrivals(_mutate(base, wrong_count))
+    assert simulate(_mutate(base, reversed_row))
+    assert ownership(_mutate(base, duplicate_row))
+    assert arrivals(_mutate(base, missing_signal)) or simulate(_mutate(base, missing_signal))
+
+
+def test_instruction_words_and_padding():
+    s = build_schedule(1, 1, 4, 1)
+    flat, counts = s.persistent_words()
+    assert len(flat) == 4 * s.max_inst * native.INST_WORDS
+    assert sum(counts) == s.num_tasks
+    words, table = s.stage_words()
+    assert sum(c for _, _, _, c in table) == s.num_tasks
+    assert Task(1, 0, 2, 3, 4, 5, 6, 7).words() == [1, 0, 2, 3, 4, 5, 6, 7]
+
+
+def test_buckets_and_auto_splits():
+    assert [batch_bucket(r) for r in range(1, 9)] == [1, 2, 4, 4, 8, 8, 8, 8]
+    with pytest.raises(ValueError):
+        batch_bucket(9)
+    assert auto_attn_splits(1) == 1 and auto_attn_splits(256) == 1 and auto_attn_splits(257) == 2
+    assert auto_attn_splits(2048) == 8 and auto_attn_splits(10 ** 6) == 16
+    assert auto_attn_splits(100, minimum=4) == 4
