@@ -1,7 +1,7 @@
 """Decode-step benchmark: device us/step and tok/s of the MI355X task-graph
 decoder vs the 1.19 GB HBM weight floor.
 
-Workload (the metric's headline case): Qwen3-0.6B
+Workload (config C3, the headline case of the metric): Qwen3-0.6B
 geometry, random-init bf16 weights (seed 0), batch 1, one random start token,
 greedy decode with the token fed back on the device (no host round trip), so
 the context grows 1 -> K. A "step" is one decode step of the batch. Timed: K
@@ -44,7 +44,7 @@ def step_bytes(contexts: list[int]) -> int:
     return WEIGHT_BYTES + sum(KV_BYTES_PER_POS * c + KV_BYTES_PER_POS + EMBED_ROW_BYTES for c in contexts)
 
 
-def build_decoder(num_layers=28, num_blocks=64, launch="persistent"):
+def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="lds_dma"):
     import torch
     from nanovllm.backends.megakernel.taskgraph import TaskGraphDecoder
     from nanovllm.backends.megakernel.weights import weights_from_synthetic
@@ -54,7 +54,7 @@ def build_decoder(num_layers=28, num_blocks=64, launch="persistent"):
     w = weights_from_synthetic(synth, device="cuda")
     kv = torch.zeros(2, num_layers, num_blocks, 256, 8, 128, dtype=torch.bfloat16, device="cuda")
     dec = TaskGraphDecoder(w, k_cache=kv[0], v_cache=kv[1], block_size=256, num_cache_blocks=num_blocks,
-                           max_model_len=2048, launch=launch)
+                           max_model_len=2048, launch=launch, persistent_variant=variant)
     return synth, w, kv, dec
 
 
@@ -122,6 +122,39 @@ def cpu_baseline(sample_steps: int = 3):
                       f"model, torch CPU fp32-accumulate restatement (oracle/qwen3_oracle.py)"}
 
 
+PERSISTENT_KERNELS = {"lds_dma": "k_persistent2", "v1": "k_persistent", "v3": "k_persistent3"}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_k_persistent2_c3.txt")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel's reading), or None."""
+
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch") and kernel in line:
+                    return int(line.split("=")[1].split()[0])
+    except OSError:
+        return None
+    return None
+
+
+def copy_calibration(nbytes: int = 1 << 30, launches: int = 4):
+    """A plain device-to-device copy of known size (read nbytes + write nbytes
+    per launch) whose FETCH_SIZE/WRITE_SIZE readings calibrate the counters."""
+
+    import torch
+
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(launches):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "launches": launches}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -131,11 +164,15 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "stages"])
+    ap.add_argument("--variant", default="lds_dma", choices=sorted(PERSISTENT_KERNELS),
+                    help="persistent kernel variant")
     ap.add_argument("--only-kernel", action="store_true", help="timed loop only (for profilers)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a 1 GiB device copy only (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode step runs TP=1 on a single MI355X; "
-              "multi-GPU data parallelism is independent replicas (see DESIGN.md). Use --gpus 1.",
+              "multi-GPU data parallelism is independent replicas of this step. Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
     import torch
@@ -143,7 +180,10 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
-    _, _, _, dec = build_decoder(num_blocks=8 * 8 + 8)
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    _, _, _, dec = build_decoder(num_blocks=8 * 8 + 8, variant=args.variant)
     start = [0] * args.batch
     elapsed, durs, contexts = time_decode(dec, args.batch, start, args.steps, args.warmup, args.mode,
                                           per_launch_events=True)
@@ -154,6 +194,12 @@ def main():
     avg_launch_ms = sum(durs) / len(durs)
     bytes_per_launch = sum(step_bytes(c) for c in contexts) / len(contexts)
     achieved = bytes_per_launch / (avg_launch_ms * 1e-3) / 1e9
+    if args.mode == "persistent":
+        kernel = f"{PERSISTENT_KERNELS[args.variant]}<{args.batch}> (one launch per decode step)"
+        traffic = measured_traffic(f"{PERSISTENT_KERNELS[args.variant]}<{args.batch}>")
+    else:
+        kernel = f"all stage kernels of one step ({args.mode})"
+        traffic = None
     result = {
         "metric": "device us/decode-step & tok/s at batch 1-8 vs 1.19GB HBM weight floor",
         "value": round(args.batch * args.steps / elapsed, 2),
@@ -175,8 +221,8 @@ def main():
                    "model": "Qwen3-0.6B geometry (random init)", "global_batch": args.batch,
                    "seq_len": args.steps, "parallelism": "single GPU (tp1)", "launch": args.mode},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "k_persistent<1> (one launch per decode step)",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel": kernel,
                      "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_ms * 1e3, 2)},
     }
     if not args.no_sweep:

@@ -16,7 +16,7 @@
 #include <string>
 #include <vector>
 
-#include "mkd_persistent.h"
+#include "mkd_pk3.h"
 
 using namespace mkd;
 
@@ -153,6 +153,8 @@ template <int B>
 int launch_persistent_b(const MkdStepDesc& d, const MkdSchedule& s, hipStream_t st) {
   if (d.flags & MKD_FLAG_PK_V1) {
     hipLaunchKernelGGL(k_persistent<B>, dim3(s.grid), dim3(NT), 0, st, d, s);
+  } else if (d.flags & MKD_FLAG_PK_V3) {
+    hipLaunchKernelGGL(k_persistent3<B>, dim3(s.grid), dim3(P3_THREADS), 0, st, d, s);
   } else {
     static bool attr_set = false;  // per instantiation; set before the first launch
     if (!attr_set) {

@@ -221,7 +221,7 @@ __device__ void task_gateup(const MkdStepDesc& d, const Ws& ws, int layer, int c
 // positions; splits are merged by the last arriving split (ticket counter).
 // Returns true when this workgroup produced the final attention output.
 // ---------------------------------------------------------------------------
-template <int B, class Sync = SyncAll>
+template <int B, class Sync = SyncAll, int NW = NWAVE>
 __device__ __forceinline__ bool task_attn(const MkdStepDesc& d, const Ws& ws, int layer, int bh, int split, int nsplit,
                           uint8_t* smem, Sync sync = Sync()) {
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
@@ -243,17 +243,18 @@ __device__ __forceinline__ bool task_attn(const MkdStepDesc& d, const Ws& ws, in
   uint16_t* kb = qb + GROUP * HD;                            // [128] roped k
   uint16_t* vb = kb + HD;                                    // [128] v
   float* mrg = reinterpret_cast<float*>(smem + 1024);        // [4 waves][2][128] + m/l
-  float* mrg_ml = mrg + NWAVE * GROUP * HD;                  // [4][2] m, [4][2] l
-  int* sh = reinterpret_cast<int*>(mrg_ml + 2 * NWAVE * GROUP);
+  float* mrg_ml = mrg + NW * GROUP * HD;                     // [NW][2] m, [NW][2] l
+  int* sh = reinterpret_cast<int*>(mrg_ml + 2 * NW * GROUP);
   int* pages = sh + 4;                                       // [MAX_PAGES] this row's physical blocks
 
   // -- the row's block table (clamped to the cache) into LDS; q/k norm + RoPE
   //    (waves 0,1: q heads 2h, 2h+1; wave 2: k; wave 3: v copy)
   {
     const int n_pages = live ? min(pos / d.block_size + 1, MAX_PAGES) : 0;
-    for (int i = t; i < n_pages; i += NT)
+    for (int i = t; i < n_pages; i += NW * 64)
       pages[i] = min(max(d.page_table[(size_t)b * d.page_stride + i], 0), d.num_blocks - 1);
     const uint16_t* row = ws.qkv() + (size_t)b * QKV_N;
+    if (wave < 4) {
     const uint16_t* src = wave < 2 ? row + (GROUP * h + wave) * HD : (wave == 2 ? row + QS + h * HD : row + QS + KVS + h * HD);
     const float x0 = bf2f(ld_co(src + lane)), x1 = bf2f(ld_co(src + lane + 64));
     uint16_t* dst = wave < 2 ? qb + wave * HD : (wave == 2 ? kb : vb);
@@ -269,6 +270,7 @@ __device__ __forceinline__ bool task_attn(const MkdStepDesc& d, const Ws& ws, in
     } else {
       dst[lane] = (uint16_t)f2bf(x0);
       dst[lane + 64] = (uint16_t)f2bf(x1);
+    }
     }
   }
   sync();
@@ -308,7 +310,7 @@ __device__ __forceinline__ bool task_attn(const MkdStepDesc& d, const Ws& ws, in
   const int dg = (lane & 15) * 8, sub = lane >> 4;
   const uint16_t* kbase = d.k_cache + layer_off;
   const uint16_t* vbase = d.v_cache + layer_off;
-  for (int t0 = p_begin + wave * 64; t0 < c_end; t0 += NWAVE * 64) {
+  for (int t0 = p_begin + wave * 64; t0 < c_end; t0 += NW * 64) {
     asm volatile("" ::: "memory");  // keep the q reads (LDS) inside the tile: hoisting them costs 128 VGPRs
     const int p = t0 + lane;
     const bool valid = p < c_end;
@@ -382,30 +384,35 @@ __device__ __forceinline__ bool task_attn(const MkdStepDesc& d, const Ws& ws, in
   }
   if (lane == 0) {
     mrg_ml[wave * GROUP + 0] = m0; mrg_ml[wave * GROUP + 1] = m1;
-    mrg_ml[NWAVE * GROUP + wave * GROUP + 0] = l0; mrg_ml[NWAVE * GROUP + wave * GROUP + 1] = l1;
+    mrg_ml[NW * GROUP + wave * GROUP + 0] = l0; mrg_ml[NW * GROUP + wave * GROUP + 1] = l1;
   }
   sync();
-  const int g = t >> 7, dd = t & 127;  // 256 threads = 2 heads x 128 dims
+  // threads 0..255 = 2 heads x 128 dims finish the merge; with NW > 4 the
+  // other threads only take part in the barriers
+  const int g = (t >> 7) & 1, dd = t & 127;
+  const bool merger = t < GROUP * HD;
   float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < NWAVE; w++) M = fmaxf(M, mrg_ml[w * GROUP + g]);
+  for (int w = 0; w < NW; w++) M = fmaxf(M, mrg_ml[w * GROUP + g]);
   float num = 0.f, den = 0.f;
   if (M != -INFINITY) {
 #pragma unroll
-    for (int w = 0; w < NWAVE; w++) {
+    for (int w = 0; w < NW; w++) {
       const float sc = expf(mrg_ml[w * GROUP + g] - M);
       num += mrg[(w * GROUP + g) * HD + dd] * sc;
-      den += mrg_ml[NWAVE * GROUP + w * GROUP + g] * sc;
+      den += mrg_ml[NW * GROUP + w * GROUP + g] * sc;
     }
   }
   uint16_t* out = ws.attn() + (size_t)b * QS + (GROUP * h + g) * HD + dd;
   if (nsplit == 1) {
-    st_co(out, (uint16_t)f2bf(num / den));
+    if (merger) st_co(out, (uint16_t)f2bf(num / den));
     return true;
   }
   float* part = ws.apart(b, h, split);
-  st_co(part + g * HD + dd, num);
-  if (dd == 0) { st_co(part + GROUP * HD + g, M); st_co(part + GROUP * HD + GROUP + g, den); }
+  if (merger) {
+    st_co(part + g * HD + dd, num);
+    if (dd == 0) { st_co(part + GROUP * HD + g, M); st_co(part + GROUP * HD + GROUP + g, den); }
+  }
   drain();
   sync();
   if (t == 0) {
@@ -417,6 +424,7 @@ __device__ __forceinline__ bool task_attn(const MkdStepDesc& d, const Ws& ws, in
   }
   sync();
   if (!sh[0]) return false;
+  if (!merger) return true;
   float Ms = -INFINITY;
   for (int s = 0; s < nsplit; s++) Ms = fmaxf(Ms, ld_co(ws.apart(b, h, s) + GROUP * HD + g));
   num = 0.f; den = 0.f;

@@ -21,6 +21,9 @@ LAYER_PTRS = 11
 
 FLAG_ADVANCE = 1
 FLAG_ZERO_FANIN = 2
+FLAG_PK_V1 = 4
+FLAG_PK_V3 = 8
+PERSISTENT_VARIANTS = {"lds_dma": 0, "v1": FLAG_PK_V1, "v3": FLAG_PK_V3}
 
 OP_NOP, OP_QKV, OP_ATTN, OP_OPROJ, OP_GATEUP, OP_DOWN, OP_LMHEAD = range(7)
 OP_NAMES = {OP_NOP: "NOP", OP_QKV: "QKV", OP_ATTN: "ATTN", OP_OPROJ: "OPROJ",

@@ -109,8 +109,13 @@ class TaskGraphDecoder:
 
     def __init__(self, weights: dict, *, k_cache, v_cache, block_size: int, num_cache_blocks: int,
                  max_model_len: int, attn_splits: int = 1, fusion_groups: int = 1,
-                 launch: str = "persistent", verbose: bool = False, debug_bounds: bool = False):
+                 launch: str = "persistent", verbose: bool = False, debug_bounds: bool = False,
+                 persistent_variant: str = "lds_dma"):
         self._lib = native.load()
+        if persistent_variant not in native.PERSISTENT_VARIANTS:
+            raise ValueError(f"persistent_variant must be one of {sorted(native.PERSISTENT_VARIANTS)}; "
+                             f"got {persistent_variant!r}")
+        self._variant_flags = native.PERSISTENT_VARIANTS[persistent_variant]
         if launch not in ("persistent", "graph"):
             raise ValueError(f"launch must be 'persistent' or 'graph'; got {launch!r}")
         self.launch = launch
@@ -218,7 +223,7 @@ class TaskGraphDecoder:
         d.rows = rows
         d.batch = geo.batch
         d.lm_slots = geo.segments[-1].lm_slots
-        d.flags = flags
+        d.flags = flags | self._variant_flags
         d.out_logits = None if logits is None else logits.data_ptr()
         return d
 

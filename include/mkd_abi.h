@@ -86,7 +86,8 @@ enum MkdInstWord {
 
 #define MKD_FLAG_ADVANCE 1u   /* after the step: input_ids[b] = token, cache_seqlens[b] += 1 */
 #define MKD_FLAG_ZERO_FANIN 2u /* set by the persistent launch: last LM task clears fan-in counters */
-#define MKD_FLAG_PK_V1 4u      /* persistent launch without LDS-DMA weight streaming (A/B reference) */
+#define MKD_FLAG_PK_V1 4u      /* persistent launch, first variant: no weight prefetch (A/B reference) */
+#define MKD_FLAG_PK_V3 8u      /* persistent launch, register-streaming variant (experimental) */
 
 typedef struct MkdStepDesc {
   /* weights (device) */

@@ -1,6 +1,6 @@
 """GPU parity: the HIP decode step vs the CPU oracle on identical weights and inputs.
 
-Tolerances (see DESIGN.md "Parity bar"):
+Tolerances:
 
 * 1-2 layers, where the inputs of every op are identical on both sides:
   logits max |diff| <= 2e-2, same greedy token, and
