@@ -49,13 +49,27 @@ constexpr size_t OFF_CTR = OFF_LMPART + 8ull * MKD_MAX_LM_SLOTS * MAXB;
 constexpr int CTR_LINE_U32 = 32;
 constexpr int CTR_ERR = 0;
 constexpr int CTR_LM_TICKET = 1;
-constexpr int CTR_COMB_BASE = 2;                                   // [layers][MAXB][NKV] tickets
+constexpr int CTR_EPOCH = 2;                                       // step counter of the tagged exchange
+constexpr int CTR_COMB_BASE = 3;                                   // [layers][MAXB][NKV] tickets
 constexpr int CTR_FANIN_BASE = CTR_COMB_BASE + MKD_NUM_LAYERS * MAXB * NKV;
 constexpr int FANIN_PER_LAYER = NKV + 4;                           // qkv[h], attn, oproj, gateup, down
 constexpr int FANIN_SUBSLOTS = 8;
 constexpr int NUM_FANIN = MKD_NUM_LAYERS * FANIN_PER_LAYER;
 constexpr int NUM_CTR_LINES = CTR_FANIN_BASE + NUM_FANIN * FANIN_SUBSLOTS;
-constexpr size_t WORKSPACE_BYTES = OFF_CTR + 128ull * NUM_CTR_LINES;
+// Tagged exchange region (persistent kernel): 64-bit words, low half = two bf16
+// values (or one fp32), high half = tag (epoch + 1) * 32 + layer. Offsets in words.
+constexpr size_t OFF_TAGGED = (OFF_CTR + 128ull * NUM_CTR_LINES + 255) & ~255ull;
+constexpr size_t TW_RES1 = 0;                                        // [MAXB][H/2]   residual after QKV-stage add
+constexpr size_t TW_RES2 = TW_RES1 + (size_t)MAXB * H / 2;           // [MAXB][H/2]   residual after GATEUP-stage add
+constexpr size_t TW_QKV = TW_RES2 + (size_t)MAXB * H / 2;            // [MAXB][QKV_N/2]
+constexpr size_t TW_ATTN = TW_QKV + (size_t)MAXB * QKV_N / 2;        // [MAXB][QS/2]
+constexpr size_t TW_O = TW_ATTN + (size_t)MAXB * QS / 2;             // [MAXB][H/2]
+constexpr size_t TW_ACT = TW_O + (size_t)MAXB * H / 2;               // [MAXB][I/2]
+constexpr size_t TW_DOWN = TW_ACT + (size_t)MAXB * I / 2;            // [MAXB][H/2]
+constexpr size_t TW_APART = TW_DOWN + (size_t)MAXB * H / 2;          // [MAXB][NKV][MAXS][PART_STRIDE] fp32
+constexpr size_t TW_LM = TW_APART + (size_t)MAXB * NKV * MAXS * PART_STRIDE;  // [MAX_LM_SLOTS][MAXB][2]
+constexpr size_t TW_WORDS = TW_LM + (size_t)MKD_MAX_LM_SLOTS * MAXB * 2;
+constexpr size_t WORKSPACE_BYTES = OFF_TAGGED + 8 * TW_WORDS;
 
 // Error codes written to the error word.
 constexpr uint32_t ERR_TIMEOUT = 1;
@@ -149,6 +163,9 @@ struct Ws {
   }
   __device__ __forceinline__ uint2* lmpart(int slot) const {
     return reinterpret_cast<uint2*>(base + OFF_LMPART) + (size_t)slot * MAXB;
+  }
+  __device__ __forceinline__ uint64_t* tw(size_t word) const {
+    return reinterpret_cast<uint64_t*>(base + OFF_TAGGED) + word;
   }
   __device__ __forceinline__ uint32_t* line(int i) const {
     return reinterpret_cast<uint32_t*>(base + OFF_CTR) + (size_t)i * CTR_LINE_U32;

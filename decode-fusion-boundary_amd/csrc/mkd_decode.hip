@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "mkd_pk3.h"
+#include "mkd_pk4.h"
 
 using namespace mkd;
 
@@ -153,6 +154,14 @@ template <int B>
 int launch_persistent_b(const MkdStepDesc& d, const MkdSchedule& s, hipStream_t st) {
   if (d.flags & MKD_FLAG_PK_V1) {
     hipLaunchKernelGGL(k_persistent<B>, dim3(s.grid), dim3(NT), 0, st, d, s);
+  } else if (d.flags & MKD_FLAG_PK_TAGGED) {
+    static bool attr_set4 = false;  // per instantiation; set before the first launch
+    if (!attr_set4) {
+      MKD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_persistent4<B>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, PkCfg<B>::LDS_BYTES));
+      attr_set4 = true;
+    }
+    hipLaunchKernelGGL(k_persistent4<B>, dim3(s.grid), dim3(PK_THREADS), PkCfg<B>::LDS_BYTES, st, d, s);
   } else if (d.flags & MKD_FLAG_PK_V3) {
     hipLaunchKernelGGL(k_persistent3<B>, dim3(s.grid), dim3(P3_THREADS), 0, st, d, s);
   } else {
@@ -254,9 +263,10 @@ uint64_t mkd_status_offset(void) { return OFF_CTR; }
 int mkd_reset_counters(const MkdStepDesc* d, void* stream) {
   if (d == nullptr || d->workspace == nullptr || d->workspace_bytes < WORKSPACE_BYTES)
     return fail(MKD_E_INVALID, "workspace missing or too small");
+  // counters, the epoch and every tagged word: no stale tag can match after a reset
   uint32_t* ctr = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(d->workspace) + OFF_CTR);
-  const int n = NUM_CTR_LINES * CTR_LINE_U32;
-  hipLaunchKernelGGL(k_reset, dim3(64), dim3(256), 0, (hipStream_t)stream, ctr, n);
+  const int n = (int)((WORKSPACE_BYTES - OFF_CTR) / 4);
+  hipLaunchKernelGGL(k_reset, dim3(256), dim3(256), 0, (hipStream_t)stream, ctr, n);
   MKD_HIP(hipGetLastError());
   return MKD_OK;
 }

@@ -23,7 +23,8 @@ FLAG_ADVANCE = 1
 FLAG_ZERO_FANIN = 2
 FLAG_PK_V1 = 4
 FLAG_PK_V3 = 8
-PERSISTENT_VARIANTS = {"lds_dma": 0, "v1": FLAG_PK_V1, "v3": FLAG_PK_V3}
+FLAG_PK_TAGGED = 16
+PERSISTENT_VARIANTS = {"lds_dma": 0, "v1": FLAG_PK_V1, "v3": FLAG_PK_V3, "tagged": FLAG_PK_TAGGED}
 
 OP_NOP, OP_QKV, OP_ATTN, OP_OPROJ, OP_GATEUP, OP_DOWN, OP_LMHEAD = range(7)
 OP_NAMES = {OP_NOP: "NOP", OP_QKV: "QKV", OP_ATTN: "ATTN", OP_OPROJ: "OPROJ",
@@ -164,9 +165,12 @@ def workspace_bytes() -> int:
 
 def workspace_layout() -> dict[str, tuple[int, int]]:
     """``name -> (byte offset, bytes)`` of the workspace regions (``csrc/mkd_common.h``).
-    Used by tests to read the kernels' intermediate activations."""
+    Used by tests to read the kernels' intermediate activations. Regions named
+    ``tw_*`` are the tagged exchange of the persistent "tagged" variant: 64-bit
+    words, low half two bf16 values (fp32 for ``tw_apart``/``tw_lm``), high half
+    the tag ``(epoch + 1) * 32 + layer``."""
 
-    maxb, h, i, qkv, qs, kv_heads = MAX_BATCH, 1024, 3072, 4096, 2048, 8
+    maxb, h, i, qkv, qs, kv_heads, layers = MAX_BATCH, 1024, 3072, 4096, 2048, 8, 28
     part_stride = 2 * 128 + 2 * 2
     regions = [
         ("resid", 2 * maxb * h * 2), ("hid_a", maxb * h * 2), ("hid_f", maxb * h * 2),
@@ -177,5 +181,31 @@ def workspace_layout() -> dict[str, tuple[int, int]]:
     for name, size in regions:
         out[name] = (off, size)
         off += size
-    out["counters"] = (off, None)
+    ctr_lines = 3 + layers * maxb * kv_heads + layers * (kv_heads + 4) * 8
+    out["counters"] = (off, 128 * ctr_lines)
+    off = (off + 128 * ctr_lines + 255) & ~255
+    words = [
+        ("tw_res1", maxb * h // 2), ("tw_res2", maxb * h // 2), ("tw_qkv", maxb * qkv // 2),
+        ("tw_attn", maxb * qs // 2), ("tw_o", maxb * h // 2), ("tw_act", maxb * i // 2),
+        ("tw_down", maxb * h // 2), ("tw_apart", maxb * kv_heads * MAX_SPLITS * part_stride),
+        ("tw_lm", MAX_LM_SLOTS * maxb * 2),
+    ]
+    for name, n in words:
+        out[name] = (off, 8 * n)
+        off += 8 * n
+    out["end"] = (off, 0)
     return out
+
+
+def decode_tagged_bf16(raw_u8, rows: int, width: int):
+    """Values of a tagged bf16 region (uint8 tensor of its bytes) as float [rows, width],
+    plus the tags [rows, width // 2]."""
+
+    import torch
+
+    words = raw_u8.view(torch.int64)[: rows * width // 2].view(rows, width // 2)
+    lo = (words & 0xFFFFFFFF)
+    vals = torch.stack([(lo & 0xFFFF), (lo >> 16) & 0xFFFF], dim=-1).reshape(rows, width)
+    as_bf16 = vals.to(torch.int16).view(torch.bfloat16).float()
+    tags = (words >> 32) & 0xFFFFFFFF
+    return as_bf16, tags

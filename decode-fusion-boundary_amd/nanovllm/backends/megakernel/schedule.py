@@ -168,6 +168,14 @@ def split_range(start: int, length: int, pieces: int) -> list[tuple[int, int]]:
     return out
 
 
+def split_pairs(start: int, length: int, pieces: int) -> list[tuple[int, int]]:
+    """Like :func:`split_range` but every block starts on an even row and holds an
+    even number of rows (``length`` and ``start`` even): the persistent kernel
+    exchanges activations as words of two bf16 values, each word from one task."""
+
+    return [(start + 2 * f, 2 * n) for f, n in split_range(0, length // 2, pieces)]
+
+
 def _qkv_segments():
     """(first row, rows, kv head) of every per-head row segment of [Wq; Wk; Wv]."""
 
@@ -199,7 +207,7 @@ def build_stages(batch: int, attn_splits: int, num_wgs: int,
         qkv = Stage(OP_QKV, layer)
         per_head = [0] * NUM_KV_HEADS
         for first, rows, h in _qkv_segments():
-            for r0, n in split_range(first, rows, -(-rows // qkv_target)):
+            for r0, n in split_pairs(first, rows, -(-rows // qkv_target)):
                 wait, cnt = prev_down if prev_down else (-1, 0)
                 qkv.tasks.append(Task(OP_QKV, layer, r0, n, 0, wait, cnt, fanin_qkv(layer, h)))
                 per_head[h] += 1
@@ -212,17 +220,17 @@ def build_stages(batch: int, attn_splits: int, num_wgs: int,
                                            fanin_qkv(layer, h), per_head[h], fanin_attn(layer)))
         stages.append(attn)
         oproj = Stage(OP_OPROJ, layer)
-        for r0, n in split_range(0, HIDDEN, num_wgs):
+        for r0, n in split_pairs(0, HIDDEN, num_wgs):
             oproj.tasks.append(Task(OP_OPROJ, layer, r0, n, 0, fanin_attn(layer),
                                     batch * NUM_KV_HEADS, fanin_oproj(layer)))
         stages.append(oproj)
         gu = Stage(OP_GATEUP, layer)
-        for c0, n in split_range(0, INTERMEDIATE, num_wgs):
+        for c0, n in split_pairs(0, INTERMEDIATE, num_wgs):
             gu.tasks.append(Task(OP_GATEUP, layer, c0, n, 0, fanin_oproj(layer),
                                  len(oproj.tasks), fanin_gateup(layer)))
         stages.append(gu)
         down = Stage(OP_DOWN, layer)
-        for r0, n in split_range(0, HIDDEN, num_wgs):
+        for r0, n in split_pairs(0, HIDDEN, num_wgs):
             down.tasks.append(Task(OP_DOWN, layer, r0, n, 0, fanin_gateup(layer),
                                    len(gu.tasks), fanin_down(layer)))
         stages.append(down)

@@ -104,6 +104,25 @@ class _Geometry:
     graph: Any = None      # captured per-op hipGraph (launch="graph")
 
 
+def _check_tagged_preconditions(segs) -> None:
+    """What the tagged-exchange kernel relies on: GEMV row blocks of even size at
+    even offsets (a word carries two values of one task), at most 32 rows per
+    block (its result tile), and an LM-head task on every workgroup of the last
+    launch (the last LM slot advances the step counter once every workgroup has
+    read it)."""
+
+    for seg in segs:
+        for row in seg.rows:
+            for t in row:
+                if t.op in (native.OP_QKV, native.OP_OPROJ, native.OP_GATEUP, native.OP_DOWN):
+                    rows = 2 * t.a1 if t.op == native.OP_GATEUP else t.a1
+                    if t.a0 % 2 or t.a1 % 2 or rows > 32:
+                        raise RuntimeError(f"task {t} does not fit the tagged exchange (even blocks of <= 32 rows)")
+    last = segs[-1]
+    if any(not any(t.op == native.OP_LMHEAD for t in row) for row in last.rows):
+        raise RuntimeError("the tagged exchange needs an LM-head task on every workgroup")
+
+
 class TaskGraphDecoder:
     """One greedy decode step of up to 8 rows on the HIP task graph."""
 
@@ -202,6 +221,8 @@ class TaskGraphDecoder:
         errors = verify(whole)
         if errors:
             raise RuntimeError("task-graph schedule failed verification: " + "; ".join(errors[:3]))
+        if self._variant_flags & native.FLAG_PK_TAGGED:
+            _check_tagged_preconditions(segs)
         persistent = []
         for seg in segs:
             flat, counts = seg.persistent_words()

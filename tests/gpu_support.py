@@ -15,7 +15,8 @@ class Harness:
     """A decoder + a paged KV cache on cuda:0, and the oracle with its own CPU cache copy."""
 
     def __init__(self, num_layers: int, num_blocks: int, *, launch="persistent", attn_splits=1,
-                 fusion_groups=1, max_model_len=2048, kv_fill_seed: int | None = None):
+                 fusion_groups=1, max_model_len=2048, kv_fill_seed: int | None = None,
+                 variant: str = "lds_dma"):
         from nanovllm.backends.megakernel.taskgraph import TaskGraphDecoder
         from nanovllm.backends.megakernel.weights import weights_from_synthetic
         from oracle.qwen3_oracle import Oracle
@@ -33,7 +34,8 @@ class Harness:
         self.kv = kv_cpu.to("cuda")
         self.dec = TaskGraphDecoder(self.w, k_cache=self.kv[0], v_cache=self.kv[1], block_size=BS,
                                     num_cache_blocks=num_blocks, max_model_len=max_model_len,
-                                    attn_splits=attn_splits, fusion_groups=fusion_groups, launch=launch)
+                                    attn_splits=attn_splits, fusion_groups=fusion_groups, launch=launch,
+                                    persistent_variant=variant)
         self.oracle = Oracle(self.synth)
 
     def step(self, ids, positions, tables, active=None, mode=None):

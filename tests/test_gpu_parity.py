@@ -27,6 +27,9 @@ pytestmark = [pytest.mark.gpu,
 
 LOGIT_TOL = 2e-2
 MODES = ["persistent", "stages", "graph"]
+VARIANTS = ["lds_dma", "tagged"]   # persistent-kernel variants
+# (launch mode, persistent variant) pairs: every launch path once
+PATHS = [("persistent", "lds_dma"), ("persistent", "tagged"), ("stages", "lds_dma"), ("graph", "lds_dma")]
 
 
 def check_tokens(toks, ref_toks, ref_logits, bound):
@@ -56,10 +59,10 @@ def ulp_row_scale(ref: torch.Tensor) -> torch.Tensor:
     return torch.pow(2.0, torch.floor(torch.log2(m)) - 7)
 
 
-@pytest.mark.parametrize("mode", MODES)
-def test_first_step_two_layers(mode):
-    print(f"case: first step, 2 layers, mode={mode}", flush=True)
-    h = Harness(num_layers=2, num_blocks=4)
+@pytest.mark.parametrize("mode,variant", PATHS)
+def test_first_step_two_layers(mode, variant):
+    print(f"case: first step, 2 layers, mode={mode} variant={variant}", flush=True)
+    h = Harness(num_layers=2, num_blocks=4, variant=variant)
     toks, logits = h.step([42], [0], [[1]], mode=mode)
     ref_toks, ref_logits = h.oracle_step([42], [0], [[1]])
     err = max_abs(logits, ref_logits)
@@ -70,14 +73,15 @@ def test_first_step_two_layers(mode):
     h.close()
 
 
+@pytest.mark.parametrize("variant", VARIANTS)
 @pytest.mark.parametrize("batch", [1, 8])
-def test_intermediates_one_layer_random_kv(batch):
+def test_intermediates_one_layer_random_kv(batch, variant):
     """Every op's output (qkv, attention, o_proj, SiLU*mul, down) within one bf16
     ulp at row scale of the oracle's, on identical inputs (1 layer, ctx ~256)."""
     from nanovllm.backends.megakernel import native
 
-    print(f"case: 1-layer intermediates, batch={batch}", flush=True)
-    h = Harness(num_layers=1, num_blocks=2 * batch + 2, kv_fill_seed=1)
+    print(f"case: 1-layer intermediates, batch={batch} variant={variant}", flush=True)
+    h = Harness(num_layers=1, num_blocks=2 * batch + 2, kv_fill_seed=1, variant=variant)
     ids = [(977 * (b + 1)) % 151936 for b in range(batch)]
     pos = [256 - (b % 3) for b in range(batch)]
     tables = [[2 * b + 3, 2 * b + 2] for b in range(batch)]
@@ -87,10 +91,18 @@ def test_intermediates_one_layer_random_kv(batch):
     assert max_abs(logits, ref_logits.float()) <= LOGIT_TOL
     assert toks == ref_toks
     layout = native.workspace_layout()
+    tagged = variant == "tagged"
     for region, width, key in (("qkv", 4096, "qkv"), ("attn", 2048, "attn"), ("hid_a", 1024, "o"),
                                ("act", 3072, "act"), ("hid_f", 1024, "down")):
-        off, size = layout[region]
-        got = h.dec._workspace[off:off + size].view(torch.bfloat16)[:batch * width].view(batch, width).float().cpu()
+        if tagged:
+            name = {"qkv": "tw_qkv", "attn": "tw_attn", "hid_a": "tw_o", "act": "tw_act", "hid_f": "tw_down"}[region]
+            off, size = layout[name]
+            got, tags = native.decode_tagged_bf16(h.dec._workspace[off:off + size].cpu(), batch, width)
+            # the first step after init runs at epoch 0: layer 0's tag is (0 + 1) * 32 + 0
+            assert bool((tags == 32).all()), f"{name}: words not written by this step"
+        else:
+            off, size = layout[region]
+            got = h.dec._workspace[off:off + size].view(torch.bfloat16)[:batch * width].view(batch, width).float().cpu()
         ref = trace[key].float()
         excess = ((got - ref).abs() / ulp_row_scale(ref)).max().item()
         print(f"  {region}: max |diff| = {excess:.2f} ulp at row scale", flush=True)
@@ -131,12 +143,13 @@ def _torch_path_logits(num_layers, kv_cpu, ids, pos, tables):
         return model.compute_logits(hidden).float().cpu()
 
 
+@pytest.mark.parametrize("variant", VARIANTS)
 @pytest.mark.parametrize("batch", [1, 4, 8])
-def test_full_depth_random_kv_context_256(batch):
+def test_full_depth_random_kv_context_256(batch, variant):
     """C2-style inputs through all 28 layers: deviation bounded by the
     torch-on-ROCm path's own deviation; tokens equal except oracle near-ties."""
-    print(f"case: 28 layers, random KV ctx 256, batch={batch}", flush=True)
-    h = Harness(num_layers=28, num_blocks=2 * batch + 2, kv_fill_seed=1)
+    print(f"case: 28 layers, random KV ctx 256, batch={batch} variant={variant}", flush=True)
+    h = Harness(num_layers=28, num_blocks=2 * batch + 2, kv_fill_seed=1, variant=variant)
     h.kv_before = h.kv_cpu.clone()
     ids = [(977 * (b + 1)) % 151936 for b in range(batch)]
     pos = [256 - (b % 3) for b in range(batch)]
@@ -155,10 +168,11 @@ def test_full_depth_random_kv_context_256(batch):
     h.close()
 
 
-def test_inactive_row_leaves_its_pages_untouched():
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_inactive_row_leaves_its_pages_untouched(variant):
     """row_active=0 skips only the KV write (reference row_contract.py:1-52)."""
-    print("case: inactive row", flush=True)
-    h = Harness(num_layers=2, num_blocks=6)
+    print(f"case: inactive row, variant={variant}", flush=True)
+    h = Harness(num_layers=2, num_blocks=6, variant=variant)
     sentinel = h.kv[:, :, 5].clone()
     toks, _ = h.step([11, 22], [0, 0], [[1], [5]], active=[1, 0])
     ref_toks, _ = h.oracle_step([11, 22], [0, 0], [[1], [5]], active=[1, 0])
@@ -168,13 +182,13 @@ def test_inactive_row_leaves_its_pages_untouched():
     h.close()
 
 
-@pytest.mark.parametrize("mode", ["persistent", "graph"])
-def test_split_kv_long_ragged_context(mode):
+@pytest.mark.parametrize("mode,variant", [("persistent", "lds_dma"), ("persistent", "tagged"), ("graph", "lds_dma")])
+def test_split_kv_long_ragged_context(mode, variant):
     """Ragged contexts up to ~1.8k positions: split-KV (auto splits) + LSE merge,
     against the oracle with the torch-relative bound (long random-KV attention
     accumulates more fp32 reordering than a first step)."""
-    print(f"case: split-KV long ragged context, mode={mode}", flush=True)
-    h = Harness(num_layers=2, num_blocks=20, kv_fill_seed=3, launch=mode)
+    print(f"case: split-KV long ragged context, mode={mode} variant={variant}", flush=True)
+    h = Harness(num_layers=2, num_blocks=20, kv_fill_seed=3, launch=mode, variant=variant)
     h.kv_before = h.kv_cpu.clone()
     ids = [5, 77, 9001]
     pos = [1800, 1023, 300]
@@ -193,10 +207,11 @@ def test_split_kv_long_ragged_context(mode):
     h.close()
 
 
-def test_greedy_decode_sixteen_steps_matches_oracle():
+@pytest.mark.parametrize("variant", VARIANTS)
+def test_greedy_decode_sixteen_steps_matches_oracle(variant):
     """C3-style autoregressive greedy decode (2 layers): the token sequence matches."""
-    print("case: 16-step greedy decode", flush=True)
-    h = Harness(num_layers=2, num_blocks=4)
+    print(f"case: 16-step greedy decode, variant={variant}", flush=True)
+    h = Harness(num_layers=2, num_blocks=4, variant=variant)
     tok_k, tok_o = 42, 42
     seq_k, seq_o = [], []
     for step in range(16):
@@ -207,4 +222,32 @@ def test_greedy_decode_sixteen_steps_matches_oracle():
         tok_k, tok_o = tk, to
     print(f"  kernel {seq_k}\n  oracle {seq_o}", flush=True)
     assert seq_k == seq_o
+    h.close()
+
+
+@pytest.mark.parametrize("mode,variant", [("persistent", "lds_dma"), ("persistent", "tagged"), ("graph", "lds_dma")])
+def test_device_resident_steps_match_host_steps(mode, variant):
+    """The benchmark's device-resident loop (token fed back and position advanced
+    by the step itself, no host sync between steps) produces the same tokens as
+    host-driven steps and the oracle, over 12 steps of batch 2 (2 layers)."""
+    print(f"case: device-resident loop, mode={mode} variant={variant}", flush=True)
+    h = Harness(num_layers=2, num_blocks=6, variant=variant)
+    ids, pos = [42, 7], [0, 3]
+    tables = [[1], [4]]
+    run = h.dec.prepare_steps(2, 64, mode=mode)
+    h.dec.stage_rows(torch.tensor(ids, dtype=torch.int64, device="cuda"),
+                     torch.tensor(pos, dtype=torch.int64, device="cuda"),
+                     torch.tensor(tables, dtype=torch.int32, device="cuda"))
+    seq_dev = []
+    for _ in range(12):
+        run()
+        seq_dev.append(h.dec.tokens(2))
+    seq_ref = []
+    cur = list(ids)
+    for step in range(12):
+        toks, _ = h.oracle_step(cur, [p + step for p in pos], tables)
+        seq_ref.append(toks)
+        cur = toks
+    print(f"  device {seq_dev}\n  oracle {seq_ref}", flush=True)
+    assert seq_dev == seq_ref
     h.close()

@@ -69,3 +69,12 @@ def test_workspace_layout_and_validation():
     desc = native.MkdStepDesc(batch=1, rows=1, num_layers=28, lm_slots=1)
     rc = lib.mkd_launch_persistent(ctypes.byref(desc), None, None)
     assert rc == -1 and b"workspace" in lib.mkd_last_error()
+
+
+def test_tagged_region_layout_matches_library():
+    """The Python view of the tagged exchange region ends exactly at the
+    library's workspace size (same constants on both sides)."""
+    lib = _lib()
+    layout = native.workspace_layout()
+    assert layout["end"][0] == lib.mkd_workspace_bytes()
+    assert layout["tw_res1"][0] % 256 == 0

@@ -97,3 +97,12 @@ def test_buckets_and_auto_splits():
     assert auto_attn_splits(1) == 1 and auto_attn_splits(256) == 1 and auto_attn_splits(257) == 2
     assert auto_attn_splits(2048) == 8 and auto_attn_splits(10 ** 6) == 16
     assert auto_attn_splits(100, minimum=4) == 4
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
+@pytest.mark.parametrize("splits", [1, 4, 16])
+def test_tagged_exchange_preconditions_at_256_cus(batch, splits):
+    """Even GEMV row blocks of <= 32 rows and an LM task on every workgroup."""
+    from nanovllm.backends.megakernel.taskgraph import _check_tagged_preconditions
+    for groups in (1, 4):
+        _check_tagged_preconditions(build_segments(batch, splits, 256, 28, groups))
