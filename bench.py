@@ -44,7 +44,7 @@ def step_bytes(contexts: list[int]) -> int:
     return WEIGHT_BYTES + sum(KV_BYTES_PER_POS * c + KV_BYTES_PER_POS + EMBED_ROW_BYTES for c in contexts)
 
 
-def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="lds_dma"):
+def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="tagged"):
     import torch
     from nanovllm.backends.megakernel.taskgraph import TaskGraphDecoder
     from nanovllm.backends.megakernel.weights import weights_from_synthetic
@@ -124,7 +124,7 @@ def cpu_baseline(sample_steps: int = 3):
 
 PERSISTENT_KERNELS = {"lds_dma": "k_persistent2", "v1": "k_persistent", "v3": "k_persistent3",
                       "tagged": "k_persistent4"}
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_k_persistent2_c3.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_c3.txt")
 
 
 def measured_traffic(kernel: str):
@@ -165,7 +165,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "stages"])
-    ap.add_argument("--variant", default="lds_dma", choices=sorted(PERSISTENT_KERNELS),
+    ap.add_argument("--variant", default="tagged", choices=sorted(PERSISTENT_KERNELS),
                     help="persistent kernel variant")
     ap.add_argument("--only-kernel", action="store_true", help="timed loop only (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",

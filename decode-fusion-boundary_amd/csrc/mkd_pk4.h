@@ -56,11 +56,30 @@ __device__ __forceinline__ uint32_t p4_tag(uint32_t epoch, int layer) { return (
 __device__ __forceinline__ uint64_t tw_make(uint32_t lo, uint32_t tag) { return (uint64_t)lo | ((uint64_t)tag << 32); }
 __device__ __forceinline__ uint32_t tw_tag(uint64_t w) { return (uint32_t)(w >> 32); }
 
+// Compute-wave barrier over an LDS counter with relaxed atomics. The LDS
+// executes each wave's operations in issue order, so LDS writes a wave made
+// before its increment are in place for any wave that has seen the count;
+// unlike a release/acquire barrier it imposes no wait on global memory, so the
+// tagged stores of the previous task stay in flight. (Each wave adds 1; the
+// value its add returns names the barrier generation.)
+struct SyncLds {
+  uint32_t* ctr;
+  __device__ __forceinline__ void operator()() const {
+    asm volatile("" ::: "memory");
+    uint32_t old = 0;
+    if ((threadIdx.x & 63) == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
+    const uint32_t target = (old / PK_CW + 1) * PK_CW;
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(0);
+    asm volatile("" ::: "memory");
+  }
+};
+
 // Compute-wave context (all fields in registers or LDS).
 struct P4 {
   Ws ws;
   uint32_t epoch;
-  SyncCW sync;
+  SyncLds sync;
   int* flags;
   float* red;
   float* res;
@@ -137,6 +156,7 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
                                               uint32_t tag_out) {
   const int t = p4_tid(), wave = t >> 6, lane = t & 63;
   const int k0 = t * 4;  // features k0..k0+3 = words 2t, 2t+1 of each row
+  const uint2 wv = *reinterpret_cast<const uint2*>(nw + k0);  // independent of the poll: issued first
   float s[B][4];
   bool ok = true;
   if (from_embed) {
@@ -178,7 +198,6 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
     if (lane == 0) c.red[wave * MAXB + b] = ss;
   }
   if (!p4_agree(c, ok)) return false;
-  const uint2 wv = *reinterpret_cast<const uint2*>(nw + k0);
   const float w4[4] = {bf_lo(wv.x), bf_hi(wv.x), bf_lo(wv.y), bf_hi(wv.y)};
 #pragma unroll
   for (int b = 0; b < B; b++) {
@@ -191,6 +210,83 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
   }
   c.sync();
   return true;
+}
+
+// Sums of each 32-lane half of a wave: the DPP butterfly of wave_sum without
+// its last (row_bcast31) step; lane 31 ends with lanes 0-31, lane 63 with 32-63.
+__device__ __forceinline__ float half_sums(float v) {
+  v += dpp_mov<0xB1>(v, 0.f);
+  v += dpp_mov<0x4E>(v, 0.f);
+  v += dpp_mov<0x141>(v, 0.f);
+  v += dpp_mov<0x140>(v, 0.f);
+  v += dpp_mov<0x142, 0xA>(v, 0.f);
+  return v;
+}
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// One LDS weight chunk (row-major rows of K bf16) times the B activations in
+// xs, over the 4 compute waves with 64 bytes of weights per lane, so that every
+// wave's loads, dot products and reductions form one short chain:
+//   K = 1024 (8 rows):  wave w -> rows 2w (lanes 0-31) and 2w+1 (lanes 32-63)
+//   K = 2048 (4 rows):  wave w -> row w
+//   K = 3072 (2 rows):  wave w -> half (w & 1) of row w >> 1; out(2 * row + half)
+// out(i, acc) gets the wave-uniform sums acc[B]; only rows < nr are reported.
+template <int B, int K, class Out>
+__device__ __forceinline__ void chunk_gemv4(const uint8_t* slot, int nr, const uint16_t* xs, Out out) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint4* x4 = reinterpret_cast<const uint4*>(xs);
+  if constexpr (K == 1024) {
+    const int half = lane >> 5, l = lane & 31;
+    const uint4* w4 = reinterpret_cast<const uint4*>(slot + (size_t)(2 * wave + half) * (K * 2));
+    uint4 wv[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) wv[c] = w4[c * 32 + l];
+    float acc[B];
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+      uint4 xv[4];  // all of this row's operand loads before its dot products
+#pragma unroll
+      for (int c = 0; c < 4; c++) xv[c] = x4[b * (K / 8) + c * 32 + l];
+      acc[b] = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; c++) acc[b] = dot8(wv[c], xv[c], acc[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < B; b++) acc[b] = half_sums(acc[b]);
+    float lo[B], hi[B];
+#pragma unroll
+    for (int b = 0; b < B; b++) { lo[b] = lane_value(acc[b], 31); hi[b] = lane_value(acc[b], 63); }
+    if (2 * wave < nr) out(2 * wave, lo);
+    if (2 * wave + 1 < nr) out(2 * wave + 1, hi);
+  } else {
+    constexpr int PARTS = K == 2048 ? 1 : 2;      // waves per row
+    constexpr int CPL = K / PARTS / 512;          // uint4 per lane: 4 or 3
+    const int row = wave / PARTS, part = wave % PARTS;
+    const uint4* w4 = reinterpret_cast<const uint4*>(slot + (size_t)row * (K * 2)) + part * (CPL * 64);
+    uint4 wv[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) wv[c] = w4[c * 64 + lane];
+    float acc[B];
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+      uint4 xv[CPL];
+#pragma unroll
+      for (int c = 0; c < CPL; c++) xv[c] = x4[b * (K / 8) + part * (CPL * 64) + c * 64 + lane];
+      acc[b] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPL; c++) acc[b] = dot8(wv[c], xv[c], acc[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < B; b++) acc[b] = wave_sum(acc[b]);
+    if (row < nr) out(PARTS * row + part, acc);
+  }
+}
+
+// Weight pointer of the layer table through scalar loads.
+__device__ __forceinline__ const uint16_t* p4_wptr(const MkdStepDesc& d, int layer, int which) {
+  return reinterpret_cast<const uint16_t*>(as_const(d.layer_ptrs)[layer * MKD_LAYER_PTRS + which]);
 }
 
 __device__ __forceinline__ int p4_rows(const Inst& w) {
@@ -211,12 +307,12 @@ __device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, c
   switch (w.op) {
     case MKD_OP_QKV: {
       const size_t out = w.a0 == 0 ? TW_RES1 : TW_NONE;
-      const uint16_t* nw = wptr(d, layer, MKD_W_LN_IN);
+      const uint16_t* nw = p4_wptr(d, layer, MKD_W_LN_IN);
       if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, out, tag);
       return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, out, tag);
     }
     case MKD_OP_GATEUP:
-      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, wptr(d, layer, MKD_W_LN_POST),
+      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST),
                               w.a0 == 0 ? TW_RES2 : TW_NONE, tag);
     case MKD_OP_OPROJ: return p4_stage_copy<B, QS>(c, TW_ATTN, tag);
     case MKD_OP_DOWN: return p4_stage_copy<B, I>(c, TW_ACT, tag);
@@ -227,44 +323,68 @@ __device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, c
   }
 }
 
-// One LDS weight chunk of a GEMV task: rows into the result tile (LM: running argmax).
+// The chunk loop of one GEMV task: one barrier per chunk hands the next LDS
+// slot over from the DMA waves; the op is fixed for the whole loop.
+// out(i, j, acc): result i of chunk j (see chunk_gemv4 for i).
+template <int B, int K, int NS, class Out>
+__device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int rows, bool aborted, uint64_t* tr,
+                                          const uint16_t* xs, Out out) {
+  constexpr int RPC = K == 1024 ? 8 : (K == 2048 ? 4 : 2);
+  uint8_t* slot = ring + (cc % NS) * SLOT_BYTES;
+  uint8_t* const ring_end = ring + NS * SLOT_BYTES;
+  for (int j = 0; j < nch; j++) {
+    raw_barrier();
+    if (j == 0 && tr != nullptr && threadIdx.x == 0) tr[2] = wall_clock64();
+    if (!aborted) chunk_gemv4<B, K>(slot, min(RPC, rows - j * RPC), xs, [&](int i, const float* acc) { out(i, j, acc); });
+    slot += SLOT_BYTES;
+    if (slot == ring_end) slot = ring;
+  }
+}
+
+// Running greedy argmax of the LM head, per row, wave-uniform (updated with
+// selects, no divergent branches).
 template <int B>
-__device__ __forceinline__ void p4_chunk(const MkdStepDesc& d, const P4& c, const Inst& w, int j, const uint8_t* slot,
-                                         LmBest& best) {
+struct LmArg {
+  float v[B];
+  int i[B];
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int b = 0; b < B; b++) { v[b] = -INFINITY; i[b] = 0x7fffffff; }
+  }
+};
+
+// All chunks of GEMV task w (results into the tile; LM: argmax into best).
+template <int B, int NS>
+__device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c, const Inst& w, uint8_t* ring, int cc,
+                                               int nch, bool aborted, uint64_t* tr, LmArg<B>& best) {
   const int lane = threadIdx.x & 63;
   const int rows = p4_rows(w);
-  auto to_res = [&](int r0) {
-    return [&, r0](int r, const float* acc) {
-      if (lane < B) c.res[(r0 + r) * MAXB + lane] = pick_lane<B>(acc, lane);
+  float* res = c.res;
+  auto to_res = [&](int rpc, int per_row) {
+    return [=](int i, int j, const float* acc) {
+      if (lane < B) res[(j * rpc * per_row + i) * MAXB + lane] = pick_lane<B>(acc, lane);
     };
   };
   switch (w.op) {
     case MKD_OP_QKV:
-    case MKD_OP_GATEUP: {
-      const int r0 = j * 8;
-      chunk_gemv<B, H>(slot, min(8, rows - r0), c.xs, to_res(r0));
-      break;
-    }
-    case MKD_OP_OPROJ: {
-      const int r0 = j * 4;
-      chunk_gemv<B, QS>(slot, min(4, rows - r0), c.xs, to_res(r0));
-      break;
-    }
-    case MKD_OP_DOWN: {
-      const int r0 = j * 2;
-      chunk_gemv<B, I>(slot, min(2, rows - r0), c.xs, to_res(r0));
-      break;
-    }
+    case MKD_OP_GATEUP: p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(8, 1)); break;
+    case MKD_OP_OPROJ: p4_chunks<B, QS, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(4, 1)); break;
+    // DOWN: two half-row partials per row, result tile entries 2 * row + half
+    case MKD_OP_DOWN: p4_chunks<B, I, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(2, 2)); break;
     case MKD_OP_LMHEAD: {
-      const int r0 = j * 8;
       uint16_t* logits = d.out_logits;
-      chunk_gemv<B, H>(slot, min(8, rows - r0), c.xs, [&](int r, const float* acc) {
-        const float v = round_bf(pick_lane<B>(acc, lane));
-        const int row = w.a0 + r0 + r;
-        if (lane < B) {
-          if (v > best.v || (v == best.v && row < best.i)) { best.v = v; best.i = row; }
-          if (logits != nullptr && lane < d.rows) logits[(size_t)lane * V + row] = (uint16_t)f2bf(v);
+      const int a0 = w.a0;
+      p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, c.xs, [&](int r, int j, const float* acc) {
+        const int row = a0 + j * 8 + r;
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+          const float v = round_bf(acc[b]);
+          const bool better = v > best.v[b] || (v == best.v[b] && row < best.i[b]);
+          best.v[b] = better ? v : best.v[b];
+          best.i[b] = better ? row : best.i[b];
         }
+        if (logits != nullptr && lane < B && lane < d.rows)
+          logits[(size_t)lane * V + row] = (uint16_t)f2bf(pick_lane<B>(acc, lane));
       });
       break;
     }
@@ -299,10 +419,19 @@ __device__ __forceinline__ void p4_store(const P4& c, const Inst& w) {
   if (w.op == MKD_OP_QKV) { base = TW_QKV; stride = QKV_N / 2; }
   else if (w.op == MKD_OP_OPROJ) { base = TW_O; stride = H / 2; }
   else { base = TW_DOWN; stride = H / 2; }
+  const bool halves = w.op == MKD_OP_DOWN;  // DOWN rows arrive as two half-row partials
   const int wpb = w.a1 / 2;
   for (int f = t; f < B * wpb; f += PK_CW * 64) {
     const int b = f / wpb, i = f - b * wpb;
-    const uint32_t lo = f2bf(c.res[(2 * i) * MAXB + b]), hi = f2bf(c.res[(2 * i + 1) * MAXB + b]);
+    float v0, v1;
+    if (halves) {
+      v0 = c.res[(4 * i) * MAXB + b] + c.res[(4 * i + 1) * MAXB + b];
+      v1 = c.res[(4 * i + 2) * MAXB + b] + c.res[(4 * i + 3) * MAXB + b];
+    } else {
+      v0 = c.res[(2 * i) * MAXB + b];
+      v1 = c.res[(2 * i + 1) * MAXB + b];
+    }
+    const uint32_t lo = f2bf(v0), hi = f2bf(v1);
     st_co(c.ws.tw(base + (size_t)b * stride + a0 / 2 + i), tw_make(lo | (hi << 16), tag));
   }
 }
@@ -310,13 +439,19 @@ __device__ __forceinline__ void p4_store(const P4& c, const Inst& w) {
 // LM-head task end: publish this slot's (max, first index) per row; the last
 // slot also reduces all slots to the greedy tokens and advances the epoch.
 template <int B>
-__device__ __forceinline__ bool p4_lm_finish(const MkdStepDesc& d, const P4& c, const Inst& w, const LmBest& best) {
+__device__ __forceinline__ bool p4_lm_finish(const MkdStepDesc& d, const P4& c, const Inst& w, const LmArg<B>& best) {
   const int t = p4_tid(), wave = t >> 6, lane = t & 63;
   const uint32_t tag = p4_tag(c.epoch, w.layer);
   float* bv = c.red;
   int* bi = reinterpret_cast<int*>(c.red + PK_CW * MAXB);
   c.sync();  // red is free (earlier users are past a barrier)
-  if (lane < B) { bv[wave * MAXB + lane] = best.v; bi[wave * MAXB + lane] = best.i; }
+  if (lane < B) {
+    float v = best.v[0]; int i = best.i[0];
+#pragma unroll
+    for (int b = 1; b < B; b++) { v = lane == b ? best.v[b] : v; i = lane == b ? best.i[b] : i; }
+    bv[wave * MAXB + lane] = v;
+    bi[wave * MAXB + lane] = i;
+  }
   c.sync();
   const int slot = w.a2;
   if (t < B) {
@@ -355,39 +490,55 @@ __device__ __forceinline__ bool p4_lm_finish(const MkdStepDesc& d, const P4& c, 
   return true;
 }
 
-// ATTN task (row b, KV head h, split of nsplit): the cached K/V of the split's
-// first tile is requested before this step's q/k/v words are polled (it does
-// not depend on them); q/k RMSNorm + RoPE, KV write (split 0 of an active
-// row), online softmax. The last split merges the others' tagged partials.
+// x[lane] + x[lane ^ 32] and x[lane] + x[lane ^ 16] on every lane (gfx950
+// permlane swaps: one VALU op instead of an LDS crossbar round trip).
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// ATTN task (row b, KV head h, split of nsplit of the row's positions).
+// Everything that does not depend on this step's q/k/v is requested before
+// its words are polled: the row's position and pages, the q/k norm weights,
+// the RoPE row and the split's first tile of cached K/V (64 positions per
+// wave). After the poll: q/k RMSNorm + RoPE in registers, the new token's K/V
+// written to its cache slot (split 0 of an active row) straight from
+// registers, scores (lane = position), softmax, P*V with the probabilities
+// broadcast through LDS (lane = 8 dims x 1 of 4 position groups), the four
+// position groups summed with permlane swaps, the four waves merged in LDS.
+// The last split folds in the other splits' tagged partials.
 template <int B>
-__device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int bh, int split, int nsplit) {
+__device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int bh, int split, int nsplit,
+                                        uint64_t* tr) {
 #ifdef MKD_PROBE_NO_ATTN
   return true;
 #endif
   const int t = p4_tid(), wave = t >> 6, lane = t & 63;
   const uint32_t tag = p4_tag(c.epoch, layer);
   const int b = bh / NKV, h = bh % NKV;
+  // row state through scalar loads (b is wave-uniform)
   bool live = b < d.rows;
-  int pos = live ? d.cache_seqlens[b] : 0;
+  int pos = live ? as_const(d.cache_seqlens)[b] : 0;
   const int bs = d.block_size;
   if (live && (pos < 0 || pos >= MKD_MAX_POSITION || pos / bs >= d.page_stride)) {
     if (t == 0) st_co(c.ws.line(CTR_ERR), ERR_BAD_INPUT);
     live = false;
     pos = 0;
   }
-  const bool active = live && d.row_active[b] != 0;
+  const bool active = live && as_const(d.row_active)[b] != 0;
+  cint32_t* table = as_const(d.page_table + (size_t)b * d.page_stride);
+  const int nblk = d.num_blocks;
   uint8_t* smem = c.attn_smem;
   uint16_t* qb = reinterpret_cast<uint16_t*>(smem);       // [2][128] roped q
   uint16_t* kb = qb + GROUP * HD;                         // [128] roped k
   uint16_t* vb = kb + HD;                                 // [128] v
-  float* mrg = reinterpret_cast<float*>(smem + 1024);     // [4][2][128]
+  float* mrg = reinterpret_cast<float*>(smem + 1024);     // [4 waves][2][128]
   float* mrg_ml = mrg + PK_CW * GROUP * HD;               // [4][2] m, [4][2] l
-  int* pages = reinterpret_cast<int*>(mrg_ml + 2 * PK_CW * GROUP) + 4;  // [MAX_PAGES]
-
-  const int n_pages = live ? min(pos / bs + 1, MAX_PAGES) : 0;
-  for (int i = t; i < n_pages; i += PK_CW * 64)
-    pages[i] = min(max(d.page_table[(size_t)b * d.page_stride + i], 0), d.num_blocks - 1);
-  c.sync();
+  float* pb = reinterpret_cast<float*>(c.xs) + wave * 128;  // [2][64] this wave's probabilities (xs is free here)
 
   const int ctx = pos + 1;
   const int chunk = ((ctx + nsplit - 1) / nsplit + 63) & ~63;
@@ -398,22 +549,49 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   const size_t layer_off = (size_t)layer * (size_t)d.kv_layer_stride + (size_t)h * HD;
   const uint16_t* kbase = d.k_cache + layer_off;
   const uint16_t* vbase = d.v_cache + layer_off;
+  // physical block of position p (clamped into the cache)
+  auto block_of = [&](int p) { return min(max(table[p / bs], 0), nblk - 1); };
   uint4 kreg[HD / 8], vreg[16];
   auto load_tile = [&](int t0) {
-    const int p = t0 + lane;
-    const int pc = p < c_end ? p : t0;
-    const uint4* krow = reinterpret_cast<const uint4*>(kbase + ((size_t)pages[pc / bs] * bs + pc % bs) * KVS);
+    if (bs % 64 == 0) {
+      // a 64-aligned tile lies in one block: one scalar lookup
+      const size_t blk_base = (size_t)block_of(t0) * bs - (t0 / bs) * bs;
+      const int p = t0 + lane < c_end ? t0 + lane : t0;
+      const uint4* krow = reinterpret_cast<const uint4*>(kbase + (blk_base + p) * KVS);
 #pragma unroll
-    for (int i = 0; i < HD / 8; i++) kreg[i] = krow[i];
+      for (int i = 0; i < HD / 8; i++) kreg[i] = krow[i];
 #pragma unroll
-    for (int it = 0; it < 16; it++) {
-      int pp = t0 + 4 * it + sub;
-      pp = pp < c_end ? pp : t0;
-      vreg[it] = *reinterpret_cast<const uint4*>(vbase + ((size_t)pages[pp / bs] * bs + pp % bs) * KVS + dg);
+      for (int it = 0; it < 16; it++) {
+        int pp = t0 + 4 * it + sub;
+        pp = pp < c_end ? pp : t0;
+        vreg[it] = *reinterpret_cast<const uint4*>(vbase + (blk_base + pp) * KVS + dg);
+      }
+    } else {
+      const int p = t0 + lane < c_end ? t0 + lane : t0;
+      const uint4* krow = reinterpret_cast<const uint4*>(kbase + ((size_t)block_of(p) * bs + p % bs) * KVS);
+#pragma unroll
+      for (int i = 0; i < HD / 8; i++) kreg[i] = krow[i];
+#pragma unroll
+      for (int it = 0; it < 16; it++) {
+        int pp = t0 + 4 * it + sub;
+        pp = pp < c_end ? pp : t0;
+        vreg[it] = *reinterpret_cast<const uint4*>(vbase + ((size_t)block_of(pp) * bs + pp % bs) * KVS + dg);
+      }
     }
   };
   const int first_t0 = p_begin + wave * 64;
   if (first_t0 < c_end) load_tile(first_t0);
+  // static operands of the norm/RoPE step, and the new token's cache slot
+  uint32_t wnw = 0;
+  float c0 = 0.f, c1 = 0.f, s0 = 0.f, s1 = 0.f;
+  if (wave < 3) {
+    wnw = reinterpret_cast<const uint32_t*>(p4_wptr(d, layer, wave < 2 ? MKD_W_Q_NORM : MKD_W_K_NORM))[lane];
+    const int j = (2 * lane) & 63;
+    const float* cs = d.rope_cos + (size_t)pos * (HD / 2);
+    const float* sn = d.rope_sin + (size_t)pos * (HD / 2);
+    c0 = cs[j]; c1 = cs[j + 1]; s0 = sn[j]; s1 = sn[j + 1];
+  }
+  const int blk_new = (split == 0 && active) ? table[pos / bs] : 0;
 
   // this step's q (waves 0, 1: heads 2h, 2h+1), k (wave 2), v (wave 3): one word per lane
   size_t src;
@@ -426,18 +604,17 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   uint32_t outw = word;
   if (wave < 3) {
     const float x0 = bf_lo(word), x1 = bf_hi(word);
-    const uint16_t* wn = wptr(d, layer, wave < 2 ? MKD_W_Q_NORM : MKD_W_K_NORM);
     const float ss = wave_sum(x0 * x0 + x1 * x1);
     const float r = 1.0f / sqrtf(ss * (1.0f / HD) + EPS);
-    const uint32_t wnw = reinterpret_cast<const uint32_t*>(wn)[lane];
     const float n0 = round_bf(round_bf(x0 * r) * bf_lo(wnw));
     const float n1 = round_bf(round_bf(x1 * r) * bf_hi(wnw));
     // rotate-half RoPE pairs dims i and i + 64: lane L holds 2L, 2L+1, lane L^32 the partners
-    const float p0 = __shfl_xor(n0, 32, 64), p1 = __shfl_xor(n1, 32, 64);
-    const int j = (2 * lane) & 63;
-    const float* cs = d.rope_cos + (size_t)pos * (HD / 2);
-    const float* sn = d.rope_sin + (size_t)pos * (HD / 2);
-    const float c0 = cs[j], c1 = cs[j + 1], s0 = sn[j], s1 = sn[j + 1];
+    // permlane32_swap(x, x) returns {[x_lo, x_lo], [x_hi, x_hi]} by 32-lane halves:
+    // the value of lane L ^ 32 is the second for L < 32 and the first otherwise
+    const auto sw0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(n0), __float_as_uint(n0), false, false);
+    const auto sw1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(n1), __float_as_uint(n1), false, false);
+    const float p0 = __uint_as_float(lane < 32 ? sw0[1] : sw0[0]);
+    const float p1 = __uint_as_float(lane < 32 ? sw1[1] : sw1[0]);
     float o0, o1;
     if (lane < 32) { o0 = n0 * c0 - p0 * s0; o1 = n1 * c1 - p1 * s1; }
     else { o0 = n0 * c0 + p0 * s0; o1 = n1 * c1 + p1 * s1; }
@@ -445,18 +622,18 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   }
   uint16_t* dst = wave < 2 ? qb + wave * HD : (wave == 2 ? kb : vb);
   reinterpret_cast<uint32_t*>(dst)[lane] = outw;
-  if (!p4_agree(c, ok)) return false;
-
-  if (split == 0 && active && t < 128) {
-    const int blk = d.page_table[(size_t)b * d.page_stride + pos / bs];
-    if (blk < 0 || blk >= d.num_blocks) {
-      if (t == 0) st_co(c.ws.line(CTR_ERR), ERR_BAD_INPUT);
+  // the new token's K (wave 2) and V (wave 3) go to their cache slot from registers
+  if (split == 0 && active && wave >= 2) {
+    if (blk_new < 0 || blk_new >= nblk) {
+      if (lane == 0) st_co(c.ws.line(CTR_ERR), ERR_BAD_INPUT);
     } else {
-      const size_t slotp = (size_t)blk * bs + pos % bs;
-      if (t < 64) reinterpret_cast<uint32_t*>(d.k_cache + layer_off + slotp * KVS)[t] = reinterpret_cast<const uint32_t*>(kb)[t];
-      else reinterpret_cast<uint32_t*>(d.v_cache + layer_off + slotp * KVS)[t - 64] = reinterpret_cast<const uint32_t*>(vb)[t - 64];
+      const size_t slotp = (size_t)blk_new * bs + pos % bs;
+      uint16_t* cache = wave == 2 ? d.k_cache : d.v_cache;
+      reinterpret_cast<uint32_t*>(cache + layer_off + slotp * KVS)[lane] = outw;
     }
   }
+  if (!p4_agree(c, ok)) return false;
+  if (tr != nullptr && t == 0) tr[2] = wall_clock64();
 
   float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
   float a0[8], a1[8];
@@ -468,38 +645,46 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     asm volatile("" ::: "memory");  // keep the q reads (LDS) inside the tile
     if (t0 != first_t0) load_tile(t0);
     const bool valid = t0 + lane < c_end;
-    float s0 = 0.f, s1 = 0.f;
+    float sc0 = 0.f, sc1 = 0.f;
 #pragma unroll
     for (int i = 0; i < HD / 8; i++) {
-      s0 = dot8(kreg[i], q0[i], s0);
-      s1 = dot8(kreg[i], q1[i], s1);
+      sc0 = dot8(kreg[i], q0[i], sc0);
+      sc1 = dot8(kreg[i], q1[i], sc1);
     }
-    s0 = valid ? s0 * ATTN_SCALE : -INFINITY;
-    s1 = valid ? s1 * ATTN_SCALE : -INFINITY;
-    const float n0 = fmaxf(m0, wave_max(s0)), n1 = fmaxf(m1, wave_max(s1));
+    sc0 = valid ? sc0 * ATTN_SCALE : -INFINITY;
+    sc1 = valid ? sc1 * ATTN_SCALE : -INFINITY;
+    const float n0 = fmaxf(m0, wave_max(sc0)), n1 = fmaxf(m1, wave_max(sc1));
     const float al0 = expf(m0 - n0), al1 = expf(m1 - n1);
-    const float e0 = expf(s0 - n0), e1 = expf(s1 - n1);
+    const float e0 = expf(sc0 - n0), e1 = expf(sc1 - n1);
     l0 = l0 * al0 + wave_sum(e0);
     l1 = l1 * al1 + wave_sum(e1);
     m0 = n0; m1 = n1;
+    // probabilities to LDS, position p = 4 * it + sub at [sub][it]: lane (dg, sub) reads 16 in a row
+    pb[(lane & 3) * 16 + (lane >> 2)] = e0;
+    pb[64 + (lane & 3) * 16 + (lane >> 2)] = e1;
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) { a0[jj] *= al0; a1[jj] *= al1; }
 #pragma unroll
-    for (int it = 0; it < 16; it++) {
-      const float w0 = __shfl(e0, 4 * it + sub, 64), w1 = __shfl(e1, 4 * it + sub, 64);
-      const uint4 v = vreg[it];
-      const float vf[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
+    for (int q = 0; q < 4; q++) {
+      const float4 x = reinterpret_cast<const float4*>(pb + sub * 16)[q];
+      const float4 y = reinterpret_cast<const float4*>(pb + 64 + sub * 16)[q];
+      const float w0[4] = {x.x, x.y, x.z, x.w}, w1[4] = {y.x, y.y, y.z, y.w};
 #pragma unroll
-      for (int jj = 0; jj < 8; jj++) { a0[jj] += w0 * vf[jj]; a1[jj] += w1 * vf[jj]; }
+      for (int e = 0; e < 4; e++) {
+        const uint4 v = vreg[4 * q + e];
+        const float vf[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) { a0[jj] += w0[e] * vf[jj]; a1[jj] += w1[e] * vf[jj]; }
+      }
     }
   }
   if (wave == 0 && p_begin <= pos && pos < p_end) {
     const uint32_t kw = reinterpret_cast<const uint32_t*>(kb)[lane];
-    const float s0 = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb)[lane], 0.f)) * ATTN_SCALE;
-    const float s1 = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb + HD)[lane], 0.f)) * ATTN_SCALE;
-    const float n0 = fmaxf(m0, s0), n1 = fmaxf(m1, s1);
+    const float t0s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb)[lane], 0.f)) * ATTN_SCALE;
+    const float t1s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb + HD)[lane], 0.f)) * ATTN_SCALE;
+    const float n0 = fmaxf(m0, t0s), n1 = fmaxf(m1, t1s);
     const float al0 = expf(m0 - n0), al1 = expf(m1 - n1);
-    const float e0 = expf(s0 - n0), e1 = expf(s1 - n1);
+    const float e0 = expf(t0s - n0), e1 = expf(t1s - n1);
     l0 = l0 * al0 + e0;
     l1 = l1 * al1 + e1;
     m0 = n0; m1 = n1;
@@ -511,17 +696,17 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
       a1[jj] = a1[jj] * al1 + (sub == 0 ? e1 * vf[jj] : 0.f);
     }
   }
+  // sum the four position groups (rows of 16 lanes), then merge the waves in LDS
 #pragma unroll
   for (int jj = 0; jj < 8; jj++) {
-    a0[jj] += __shfl_xor(a0[jj], 16, 64); a0[jj] += __shfl_xor(a0[jj], 32, 64);
-    a1[jj] += __shfl_xor(a1[jj], 16, 64); a1[jj] += __shfl_xor(a1[jj], 32, 64);
+    a0[jj] = xor32_sum(xor16_sum(a0[jj]));
+    a1[jj] = xor32_sum(xor16_sum(a1[jj]));
   }
   if (lane < 16) {
-#pragma unroll
-    for (int jj = 0; jj < 8; jj++) {
-      mrg[(wave * GROUP + 0) * HD + lane * 8 + jj] = a0[jj];
-      mrg[(wave * GROUP + 1) * HD + lane * 8 + jj] = a1[jj];
-    }
+    float4* m0p = reinterpret_cast<float4*>(mrg + (wave * GROUP + 0) * HD + lane * 8);
+    float4* m1p = reinterpret_cast<float4*>(mrg + (wave * GROUP + 1) * HD + lane * 8);
+    m0p[0] = make_float4(a0[0], a0[1], a0[2], a0[3]); m0p[1] = make_float4(a0[4], a0[5], a0[6], a0[7]);
+    m1p[0] = make_float4(a1[0], a1[1], a1[2], a1[3]); m1p[1] = make_float4(a1[4], a1[5], a1[6], a1[7]);
   }
   if (lane == 0) {
     mrg_ml[wave * GROUP + 0] = m0; mrg_ml[wave * GROUP + 1] = m1;
@@ -555,8 +740,8 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
       return true;
     }
     // last split: fold in the other splits' partials (online, -inf = empty split)
-    for (int s = 0; s < nsplit - 1; s++) {
-      const size_t ps = pbase + (size_t)s * PART_STRIDE;
+    for (int sp = 0; sp < nsplit - 1; sp++) {
+      const size_t ps = pbase + (size_t)sp * PART_STRIDE;
       uint64_t e[3];
       ok = ok && poll_tagged<3>(
                      [&](int k) {
@@ -581,50 +766,139 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
 }
 
 // ---- DMA waves -------------------------------------------------------------
-template <int B, int K>
-__device__ __forceinline__ void p4_dma_task(const uint16_t* base0, const uint16_t* base1, size_t stride, int rows,
-                                            uint8_t* ring, int dw, int& c) {
-  using Cfg = PkCfg<B>;
+// A decoded task as one DMA wave sees it (all wave-uniform). A chunk is 16
+// 1-KiB units (K = 3072: 12) of whole rows; unit u of a chunk lands at LDS
+// offset u * 1 KiB of its slot. In every full chunk this wave's units form an
+// arithmetic sequence in both the source and the slot, so a full chunk costs
+// a pointer bump and 4 (K = 3072: 3) copies:
+//   K = 1024: units dw + 4k   -> rows 2k + (dw >> 1), half (dw & 1) of the row
+//             (GATEUP: dw >> 1 picks the gate or up matrix, k the channel)
+//   K = 2048: units dw + 4k   -> row k, quarter dw
+//   K = 3072: units 3dw + k   -> row dw >> 1, sixth 3 (dw & 1) + k
+// A short last chunk (rows not a multiple of the chunk's) takes the general
+// path, which repeats the task's last unit to keep the copy count.
+struct DmaTask {
+  int kind;              // 0: K = 1024, 1: K = 2048, 2: K = 3072
+  int nch;               // chunks (0: no weights)
+  int nfull;             // leading full chunks
+  int units;             // 1-KiB units of the task's weight rows
+  int stride;            // elements between consecutive rows (per channel for GATEUP)
+  const uint16_t* b0;    // row 0 (GATEUP: gate rows)
+  const uint16_t* b1;    // GATEUP: up rows, else null
+  const uint16_t* src;   // this wave's first unit of the next full chunk
+  int64_t kstep;         // elements between this wave's units within a chunk
+  int64_t cstep;         // elements between chunks
+  int lds0, ldsk;        // slot offset of this wave's first unit, and between its units (bytes)
+};
+
+__device__ __forceinline__ DmaTask dma_decode(cuint64_t* lp, const uint16_t* emb, const Inst& w, int dw) {
+  auto W = [&](int which) { return reinterpret_cast<const uint16_t*>(lp[w.layer * MKD_LAYER_PTRS + which]); };
+  const int a0 = w.a0, a1 = w.a1;
+  DmaTask t{};
+  t.b1 = nullptr;
+  switch (w.op) {
+    case MKD_OP_QKV:
+      t.b0 = a0 < QS ? W(MKD_W_Q) + (size_t)a0 * H
+                     : (a0 < QS + KVS ? W(MKD_W_K) + (size_t)(a0 - QS) * H : W(MKD_W_V) + (size_t)(a0 - QS - KVS) * H);
+      t.kind = 0; t.units = 2 * a1; t.stride = H;
+      break;
+    case MKD_OP_LMHEAD:
+      t.b0 = emb + (size_t)a0 * H;
+      t.kind = 0; t.units = 2 * a1; t.stride = H;
+      break;
+    case MKD_OP_GATEUP:
+      t.b0 = W(MKD_W_GATE) + (size_t)a0 * H;
+      t.b1 = W(MKD_W_UP) + (size_t)a0 * H;
+      t.kind = 0; t.units = 4 * a1; t.stride = H;
+      break;
+    case MKD_OP_OPROJ:
+      t.b0 = W(MKD_W_O) + (size_t)a0 * QS;
+      t.kind = 1; t.units = 4 * a1; t.stride = QS;
+      break;
+    case MKD_OP_DOWN:
+      t.b0 = W(MKD_W_DOWN) + (size_t)a0 * I;
+      t.kind = 2; t.units = 6 * a1; t.stride = I;
+      break;
+    default:
+      t.nch = 0;
+      return t;
+  }
+  const int upc = t.kind == 2 ? 12 : 16;
+  t.nch = (t.units + upc - 1) / upc;
+  t.nfull = t.units / upc;
+  if (t.kind == 0) {
+    if (t.b1 != nullptr) {
+      t.src = ((dw >> 1) ? t.b1 : t.b0) + (dw & 1) * 512;
+      t.kstep = t.stride;
+      t.cstep = 4 * (int64_t)t.stride;
+    } else {
+      t.src = t.b0 + (size_t)(dw >> 1) * t.stride + (dw & 1) * 512;
+      t.kstep = 2 * (int64_t)t.stride;
+      t.cstep = 8 * (int64_t)t.stride;
+    }
+    t.lds0 = dw * 1024; t.ldsk = 4096;
+  } else if (t.kind == 1) {
+    t.src = t.b0 + dw * 512;
+    t.kstep = t.stride;
+    t.cstep = 4 * (int64_t)t.stride;
+    t.lds0 = dw * 1024; t.ldsk = 4096;
+  } else {
+    t.src = t.b0 + (size_t)(dw >> 1) * t.stride + 3 * (dw & 1) * 512;
+    t.kstep = 512;
+    t.cstep = 2 * (int64_t)t.stride;
+    t.lds0 = 3 * dw * 1024; t.ldsk = 1024;
+  }
+  return t;
+}
+
+// Copy chunk j of task t into `slot` (this DMA wave's share).
+template <int K>
+__device__ __forceinline__ void dma_issue(DmaTask& t, int j, uint8_t* slot, int dw) {
   constexpr int PR = K / 512;       // 1-KiB units per row
-  constexpr int RPC = 16 / PR;      // rows per chunk
-  constexpr int UPC = RPC * PR;     // units per chunk
-  constexpr int LPW = UPC / 4;      // copies per DMA wave per chunk (4, or 3 for K = 3072)
+  constexpr int UPC = (16 / PR) * PR;
+  constexpr int LPW = UPC / 4;      // copies per DMA wave per chunk
   const int lane = threadIdx.x & 63;
-  const int units = rows * PR;
-  for (int u0 = 0; u0 < units; u0 += UPC) {
-    uint8_t* slot = ring + (c % Cfg::NS) * SLOT_BYTES;
+#ifndef MKD_PROBE_SKIP_DMA
+  if (j < t.nfull) {
 #pragma unroll
-    for (int k = 0; k < LPW; k++) {
-      const int u = min(u0 + dw + 4 * k, units - 1);  // a short last chunk repeats its last unit
-      const int r = u / PR, p = u - r * PR;
-      const uint16_t* row = base1 != nullptr ? ((r & 1) ? base1 : base0) + (size_t)(r >> 1) * stride
-                                             : base0 + (size_t)r * stride;
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)(row + p * 512 + lane * 8), (lds_void_t*)(slot + (u - u0) * 1024),
-                                       16, 0, 0);
-    }
-    if (c >= Cfg::D) {
-      waitcnt_vm<3 * Cfg::D>();  // chunk c - D has landed (every later chunk issued >= 3 copies)
-      raw_barrier();             // ... and is handed to the compute waves
-    }
-    c++;
+    for (int k = 0; k < LPW; k++)
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(t.src + k * t.kstep + lane * 8),
+                                       (lds_void_t*)(slot + t.lds0 + k * t.ldsk), 16, 0, 0);
+    t.src += t.cstep;
+    return;
   }
+  const int u0 = j * UPC;
+#pragma unroll
+  for (int k = 0; k < LPW; k++) {
+    const int u = min(u0 + dw + 4 * k, t.units - 1);
+    const int r = u / PR, p = u - r * PR;
+    const uint16_t* row = t.b1 != nullptr ? ((r & 1) ? t.b1 : t.b0) + (size_t)(r >> 1) * t.stride
+                                          : t.b0 + (size_t)r * t.stride;
+    __builtin_amdgcn_global_load_lds((gbl_void_t*)(row + p * 512 + lane * 8), (lds_void_t*)(slot + (u - u0) * 1024),
+                                     16, 0, 0);
+  }
+#else
+  (void)t; (void)j; (void)slot; (void)dw; (void)lane;
+#endif
 }
 
+// s_waitcnt vmcnt(3 * later) for a runtime later in [0, M]: chunk r has landed
+// when at most the copies of the `later` chunks issued after it are pending
+// (each chunk issues at least 3 copies per DMA wave).
 template <int M>
-__device__ __forceinline__ void p4_dma_tail(int c) {
-  // chunks c-1-M .. c-1 are still to be handed over; chunk c-1-M has M later chunks
-  if constexpr (M >= 0) {
-    if (M < c) {
-      waitcnt_vm<3 * M>();
-      raw_barrier();
-    }
-    p4_dma_tail<M - 1>(c);
-  }
+__device__ __forceinline__ void wait_chunk(int later) {
+  if (later >= M) { waitcnt_vm<3 * M>(); return; }
+  if constexpr (M > 0) wait_chunk<M - 1>(later);
 }
 
+// The DMA waves: keep D chunks in flight; for each chunk r, wait until it has
+// landed, hand it over (barrier r), then issue chunk r + D. Decoding a new
+// task (scalar loads) therefore overlaps the compute waves' work on chunk r
+// instead of delaying the hand-over of chunk r + 1. Chunk r + D goes to the
+// slot of chunk r - 2, which the compute waves finished before barrier r - 1.
 template <int B>
 __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* embed, const int32_t* row,
-                                    int n_inst_arg, uint8_t* ring_arg, int dw_arg) {
+                                    int n_inst_arg, uint8_t* ring_arg, int dw_arg, uint8_t* ws_arg) {
   using Cfg = PkCfg<B>;
   cuint64_t* lp = as_const(uniform_ptr(layer_ptrs));
   const uint16_t* emb = uniform_ptr(embed);
@@ -632,29 +906,36 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
   const int n = __builtin_amdgcn_readfirstlane(n_inst_arg);
   uint8_t* ring = uniform_ptr(ring_arg);
   const int dw = __builtin_amdgcn_readfirstlane(dw_arg);
-  int c = 0;
-  for (int i = 0; i < n; i++) {
-    const Inst w = load_inst(crow + i * MKD_INST_WORDS);
-    const int a0 = w.a0, a1 = w.a1;
-    auto W = [&](int which) { return reinterpret_cast<const uint16_t*>(lp[w.layer * MKD_LAYER_PTRS + which]); };
-    switch (w.op) {
-      case MKD_OP_QKV: {
-        const uint16_t* base = a0 < QS ? W(MKD_W_Q) + (size_t)a0 * H
-                                       : (a0 < QS + KVS ? W(MKD_W_K) + (size_t)(a0 - QS) * H
-                                                        : W(MKD_W_V) + (size_t)(a0 - QS - KVS) * H);
-        p4_dma_task<B, H>(base, nullptr, H, a1, ring, dw, c);
-        break;
-      }
-      case MKD_OP_OPROJ: p4_dma_task<B, QS>(W(MKD_W_O) + (size_t)a0 * QS, nullptr, QS, a1, ring, dw, c); break;
-      case MKD_OP_GATEUP:
-        p4_dma_task<B, H>(W(MKD_W_GATE) + (size_t)a0 * H, W(MKD_W_UP) + (size_t)a0 * H, H, 2 * a1, ring, dw, c);
-        break;
-      case MKD_OP_DOWN: p4_dma_task<B, I>(W(MKD_W_DOWN) + (size_t)a0 * I, nullptr, I, a1, ring, dw, c); break;
-      case MKD_OP_LMHEAD: p4_dma_task<B, H>(emb + (size_t)a0 * H, nullptr, H, a1, ring, dw, c); break;
-      default: break;
+  (void)ws_arg;  // workspace base (debug hooks)
+  int ti = 0, tj = 0, issued = 0;
+  DmaTask cur{};
+  auto next_task = [&]() {
+    for (; ti < n; ti++) {
+      cur = dma_decode(lp, emb, load_inst(crow + ti * MKD_INST_WORDS), dw);
+      if (cur.nch > 0) return;
     }
+    cur.nch = 0;
+  };
+  auto issue_one = [&]() {
+    if (cur.nch == 0) return;
+    uint8_t* slot = ring + (issued % Cfg::NS) * SLOT_BYTES;
+    if (cur.kind == 0) dma_issue<H>(cur, tj, slot, dw);
+    else if (cur.kind == 1) dma_issue<QS>(cur, tj, slot, dw);
+    else dma_issue<I>(cur, tj, slot, dw);
+    issued++;
+    if (++tj == cur.nch) {
+      tj = 0;
+      ti++;
+      next_task();
+    }
+  };
+  next_task();
+  for (int k = 0; k < Cfg::D; k++) issue_one();
+  for (int r = 0; r < issued; r++) {
+    wait_chunk<Cfg::D - 1>(issued - r - 1);
+    raw_barrier();
+    issue_one();
   }
-  p4_dma_tail<Cfg::D - 1>(c);
 }
 
 template <int B>
@@ -676,38 +957,38 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
   }
   __syncthreads();
   if (wave >= PK_CW) {
-    p4_dma<B>(d.layer_ptrs, d.embed, row, n_inst, ring, wave - PK_CW);
+    p4_dma<B>(d.layer_ptrs, d.embed, row, n_inst, ring, wave - PK_CW, reinterpret_cast<uint8_t*>(d.workspace));
     return;
   }
-  const P4 c{ws, (uint32_t)flags[1], SyncCW{reinterpret_cast<uint32_t*>(scratch)}, flags,
+  const P4 c{ws, (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch)}, flags,
              reinterpret_cast<float*>(scratch + P4_SCR_RED), reinterpret_cast<float*>(scratch + P4_SCR_RES), xs,
              scratch + P4_SCR_ATTN};
   bool aborted = false;
   int cc = 0;
   cint32_t* crow = as_const(row);
+  Inst w_next = n_inst > 0 ? load_inst(crow) : Inst{};
   for (int i = 0; i < n_inst; i++) {
-    const Inst w = load_inst(crow + i * MKD_INST_WORDS);
+    const Inst w = w_next;
+    if (i + 1 < n_inst) w_next = load_inst(crow + (i + 1) * MKD_INST_WORDS);  // in flight during this task
     uint64_t* tr = d.trace != nullptr ? d.trace + ((size_t)blockIdx.x * s.max_inst + i) * 4 : nullptr;
     if (tr != nullptr && threadIdx.x == 0) tr[0] = wall_clock64();
     if (w.op == MKD_OP_ATTN) {
-      if (!aborted) aborted = !p4_attn<B>(d, c, w.layer, w.a0, w.a1, w.a2);
-      if (tr != nullptr && threadIdx.x == 0) { tr[1] = tr[0]; tr[2] = tr[0]; tr[3] = wall_clock64(); }
+      if (!aborted) aborted = !p4_attn<B>(d, c, w.layer, w.a0, w.a1, w.a2, tr);
+      if (tr != nullptr && threadIdx.x == 0) tr[3] = wall_clock64();
       continue;
     }
     const int nch = p4_chunks(w);
     if (nch == 0) continue;
-    if (!aborted && p4_rows(w) > P4_MAX_ROWS && w.op != MKD_OP_LMHEAD) {
+    if (!aborted && w.op != MKD_OP_LMHEAD && p4_rows(w) * (w.op == MKD_OP_DOWN ? 2 : 1) > P4_MAX_ROWS) {
       if (threadIdx.x == 0) st_co(ws.line(CTR_ERR), ERR_BAD_INST);
       aborted = true;
     }
     if (!aborted) aborted = !p4_prologue<B>(d, c, w);
-    if (tr != nullptr && threadIdx.x == 0) { tr[1] = wall_clock64(); tr[2] = tr[1]; }
-    LmBest best{-INFINITY, 0x7fffffff};
-    for (int j = 0; j < nch; j++, cc++) {
-      raw_barrier();
-      if (aborted) continue;  // keep pairing barriers with the DMA waves
-      p4_chunk<B>(d, c, w, j, ring + (cc % Cfg::NS) * SLOT_BYTES, best);
-    }
+    if (tr != nullptr && threadIdx.x == 0) tr[1] = wall_clock64();
+    LmArg<B> best;
+    best.reset();
+    p4_task_chunks<B, Cfg::NS>(d, c, w, ring, cc, nch, aborted, tr, best);
+    cc += nch;
     if (!aborted) {
       if (w.op == MKD_OP_LMHEAD) aborted = !p4_lm_finish<B>(d, c, w, best);
       else p4_store<B>(c, w);

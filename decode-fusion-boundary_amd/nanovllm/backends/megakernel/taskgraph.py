@@ -115,7 +115,8 @@ def _check_tagged_preconditions(segs) -> None:
         for row in seg.rows:
             for t in row:
                 if t.op in (native.OP_QKV, native.OP_OPROJ, native.OP_GATEUP, native.OP_DOWN):
-                    rows = 2 * t.a1 if t.op == native.OP_GATEUP else t.a1
+                    # result-tile entries: GATEUP has 2 rows per channel, DOWN 2 partials per row
+                    rows = 2 * t.a1 if t.op in (native.OP_GATEUP, native.OP_DOWN) else t.a1
                     if t.a0 % 2 or t.a1 % 2 or rows > 32:
                         raise RuntimeError(f"task {t} does not fit the tagged exchange (even blocks of <= 32 rows)")
     last = segs[-1]
@@ -129,7 +130,7 @@ class TaskGraphDecoder:
     def __init__(self, weights: dict, *, k_cache, v_cache, block_size: int, num_cache_blocks: int,
                  max_model_len: int, attn_splits: int = 1, fusion_groups: int = 1,
                  launch: str = "persistent", verbose: bool = False, debug_bounds: bool = False,
-                 persistent_variant: str = "lds_dma"):
+                 persistent_variant: str = "tagged"):
         self._lib = native.load()
         if persistent_variant not in native.PERSISTENT_VARIANTS:
             raise ValueError(f"persistent_variant must be one of {sorted(native.PERSISTENT_VARIANTS)}; "
