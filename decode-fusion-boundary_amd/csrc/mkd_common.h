@@ -58,15 +58,20 @@ constexpr int NUM_FANIN = MKD_NUM_LAYERS * FANIN_PER_LAYER;
 constexpr int NUM_CTR_LINES = CTR_FANIN_BASE + NUM_FANIN * FANIN_SUBSLOTS;
 // Tagged exchange region (persistent kernel): 64-bit words, low half = two bf16
 // values (or one fp32), high half = tag (epoch + 1) * 32 + layer. Offsets in words.
+// The buffers every workgroup reads come in TW_NREP replicas (one per XCD, so
+// each is polled by one XCD's workgroups); the QKV words, split partials and LM
+// partials have a single copy.
 constexpr size_t OFF_TAGGED = (OFF_CTR + 128ull * NUM_CTR_LINES + 255) & ~255ull;
 constexpr size_t TW_RES1 = 0;                                        // [MAXB][H/2]   residual after QKV-stage add
 constexpr size_t TW_RES2 = TW_RES1 + (size_t)MAXB * H / 2;           // [MAXB][H/2]   residual after GATEUP-stage add
-constexpr size_t TW_QKV = TW_RES2 + (size_t)MAXB * H / 2;            // [MAXB][QKV_N/2]
-constexpr size_t TW_ATTN = TW_QKV + (size_t)MAXB * QKV_N / 2;        // [MAXB][QS/2]
+constexpr size_t TW_ATTN = TW_RES2 + (size_t)MAXB * H / 2;           // [MAXB][QS/2]
 constexpr size_t TW_O = TW_ATTN + (size_t)MAXB * QS / 2;             // [MAXB][H/2]
 constexpr size_t TW_ACT = TW_O + (size_t)MAXB * H / 2;               // [MAXB][I/2]
 constexpr size_t TW_DOWN = TW_ACT + (size_t)MAXB * I / 2;            // [MAXB][H/2]
-constexpr size_t TW_APART = TW_DOWN + (size_t)MAXB * H / 2;          // [MAXB][NKV][MAXS][PART_STRIDE] fp32
+constexpr size_t TW_GROUP = TW_DOWN + (size_t)MAXB * H / 2;          // words of one replica
+constexpr int TW_NREP = 8;
+constexpr size_t TW_QKV = TW_GROUP * TW_NREP;                        // [MAXB][QKV_N/2]
+constexpr size_t TW_APART = TW_QKV + (size_t)MAXB * QKV_N / 2;       // [MAXB][NKV][MAXS][PART_STRIDE] fp32
 constexpr size_t TW_LM = TW_APART + (size_t)MAXB * NKV * MAXS * PART_STRIDE;  // [MAX_LM_SLOTS][MAXB][2]
 constexpr size_t TW_WORDS = TW_LM + (size_t)MKD_MAX_LM_SLOTS * MAXB * 2;
 constexpr size_t WORKSPACE_BYTES = OFF_TAGGED + 8 * TW_WORDS;

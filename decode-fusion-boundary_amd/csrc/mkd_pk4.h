@@ -52,6 +52,22 @@ __device__ __forceinline__ int p4_tid() {
   return v;
 }
 
+// XCD (accelerator complex die) of the executing compute unit: HW_REG_XCC_ID bits [3:0].
+__device__ __forceinline__ int p4_xcc_id() {
+  return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));
+}
+// Store for a consumer on the same XCD: a plain store lands in the XCD's shared
+// L2, where the consumer's device-coherent load finds it (a write-through store
+// would first have to reach the memory-side cache, ~5x slower measured).
+__device__ __forceinline__ void st_local(uint64_t* p, uint64_t v) {
+  asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
+// A word every workgroup reads: one write-through copy per XCD replica.
+__device__ __forceinline__ void st_all(const Ws& ws, size_t word, uint64_t v) {
+#pragma unroll
+  for (int r = 0; r < TW_NREP; r++) st_co(ws.tw(word + (size_t)r * TW_GROUP), v);
+}
+
 __device__ __forceinline__ uint32_t p4_tag(uint32_t epoch, int layer) { return (epoch + 1u) * 32u + (uint32_t)layer; }
 __device__ __forceinline__ uint64_t tw_make(uint32_t lo, uint32_t tag) { return (uint64_t)lo | ((uint64_t)tag << 32); }
 __device__ __forceinline__ uint32_t tw_tag(uint64_t w) { return (uint32_t)(w >> 32); }
@@ -78,6 +94,8 @@ struct SyncLds {
 // Compute-wave context (all fields in registers or LDS).
 struct P4 {
   Ws ws;
+  int rep;          // replica of the all-read buffers this workgroup polls (= its XCD slot)
+  int xcc;          // XCD this workgroup runs on (hardware register)
   uint32_t epoch;
   SyncLds sync;
   int* flags;
@@ -87,19 +105,27 @@ struct P4 {
   uint8_t* attn_smem;
 };
 
-// Load N tagged words (addr(k), k < N) and spin until each carries `tag`.
-// Returns false on a timeout (which it reports) or when another workgroup has
-// reported an error.
+// First round of a poll: issue the loads (returned in a[]). Issuing it before
+// a task's other loads matters: loads complete in issue order, so a check of
+// a[] then waits only for loads issued before it.
 template <int N, class Addr>
-__device__ __forceinline__ bool poll_tagged(Addr addr, uint64_t (&v)[N], uint32_t tag, const Ws& ws) {
+__device__ __forceinline__ void poll_issue(Addr addr, uint64_t (&a)[N]) {
 #pragma unroll
-  for (int k = 0; k < N; k++) v[k] = ld_co(addr(k));
+  for (int k = 0; k < N; k++) a[k] = ld_co(addr(k));
+}
+// Check the first round and keep polling until every word carries `tag`
+// (one round in flight: measured no slower than two, with half the traffic).
+template <int N, class Addr>
+__device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_t (&v)[N], uint32_t tag,
+                                            const Ws& ws) {
+  static_assert(N <= 32, "pending mask");
+  uint32_t pending = N == 32 ? ~0u : ((1u << N) - 1u);
   uint64_t t0 = 0;
   for (uint32_t spin = 0;; spin++) {
-    bool ok = true;
 #pragma unroll
-    for (int k = 0; k < N; k++) ok &= tw_tag(v[k]) == tag;
-    if (ok) return true;
+    for (int k = 0; k < N; k++)
+      if (((pending >> k) & 1u) && tw_tag(a[k]) == tag) { v[k] = a[k]; pending &= ~(1u << k); }
+    if (pending == 0u) return true;
     if ((spin & 63u) == 0u) {
       const uint64_t now = wall_clock64();
       if (spin == 0) t0 = now;
@@ -112,8 +138,17 @@ __device__ __forceinline__ bool poll_tagged(Addr addr, uint64_t (&v)[N], uint32_
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
     for (int k = 0; k < N; k++)
-      if (tw_tag(v[k]) != tag) v[k] = ld_co(addr(k));
+      if ((pending >> k) & 1u) a[k] = ld_co(addr(k));
   }
+}
+// Load N tagged words (addr(k), k < N) and spin until each carries `tag`.
+// Returns false on a timeout (which it reports) or when another workgroup
+// has reported an error.
+template <int N, class Addr>
+__device__ __forceinline__ bool poll_tagged(Addr addr, uint64_t (&v)[N], uint32_t tag, const Ws& ws) {
+  uint64_t a[N];
+  poll_issue<N>(addr, a);
+  return poll_finish<N>(addr, a, v, tag, ws);
 }
 
 // Compute-wave barrier that also ORs an abort flag over the four waves.
@@ -133,7 +168,7 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
   constexpr int PER = B * (K / 2) / 256;  // words per thread
   constexpr int NB = largest_divisor_le8(PER);
   const int t = p4_tid();
-  const uint64_t* src = c.ws.tw(base);
+  const uint64_t* src = c.ws.tw(base + (size_t)c.rep * TW_GROUP);
   uint32_t* dst = reinterpret_cast<uint32_t*>(c.xs);
   bool ok = true;
 #pragma unroll
@@ -153,12 +188,22 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
 template <int B>
 __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c, bool from_embed, size_t hid,
                                               size_t resid, uint32_t tag_in, const uint16_t* nw, size_t res_out,
-                                              uint32_t tag_out) {
+                                              uint32_t tag_out, bool res_owner) {
   const int t = p4_tid(), wave = t >> 6, lane = t & 63;
   const int k0 = t * 4;  // features k0..k0+3 = words 2t, 2t+1 of each row
-  const uint2 wv = *reinterpret_cast<const uint2*>(nw + k0);  // independent of the poll: issued first
   float s[B][4];
   bool ok = true;
+  // rows in groups of G (two rows at a time keeps the in-flight poll registers small)
+  constexpr int G = B < 2 ? B : 2;
+  auto addr = [&](int b0) {
+    return [=](int k) {
+      return c.ws.tw(((k & 2) ? resid : hid) + (size_t)c.rep * TW_GROUP + (size_t)(b0 + (k >> 2)) * (H / 2) + 2 * t +
+                     (k & 1));
+    };
+  };
+  uint64_t first[4 * G];
+  if (!from_embed) poll_issue<4 * G>(addr(0), first);    // before any other load of this task
+  const uint2 wv = *reinterpret_cast<const uint2*>(nw + k0);
   if (from_embed) {
 #pragma unroll
     for (int b = 0; b < B; b++) {
@@ -171,24 +216,31 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
       s[b][0] = bf_lo(e.x); s[b][1] = bf_hi(e.x); s[b][2] = bf_lo(e.y); s[b][3] = bf_hi(e.y);
     }
   } else {
-    uint64_t v[4 * B];
-    ok = poll_tagged<4 * B>(
-        [&](int k) { return c.ws.tw(((k & 2) ? resid : hid) + (size_t)(k >> 2) * (H / 2) + 2 * t + (k & 1)); }, v,
-        tag_in, c.ws);
 #pragma unroll
-    for (int b = 0; b < B; b++) {
-      const uint32_t h0 = (uint32_t)v[4 * b], h1 = (uint32_t)v[4 * b + 1];
-      const uint32_t r0 = (uint32_t)v[4 * b + 2], r1 = (uint32_t)v[4 * b + 3];
-      s[b][0] = bf_lo(h0) + bf_lo(r0); s[b][1] = bf_hi(h0) + bf_hi(r0);
-      s[b][2] = bf_lo(h1) + bf_lo(r1); s[b][3] = bf_hi(h1) + bf_hi(r1);
+    for (int b0 = 0; b0 < B; b0 += G) {
+      uint64_t v[4 * G];
+      if (b0 == 0) {
+        ok = poll_finish<4 * G>(addr(0), first, v, tag_in, c.ws);
+      } else {
+        ok = ok && poll_tagged<4 * G>(addr(b0), v, tag_in, c.ws);
+      }
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        const int b = b0 + g;
+        const uint32_t h0 = (uint32_t)v[4 * g], h1 = (uint32_t)v[4 * g + 1];
+        const uint32_t r0 = (uint32_t)v[4 * g + 2], r1 = (uint32_t)v[4 * g + 3];
+        s[b][0] = bf_lo(h0) + bf_lo(r0); s[b][1] = bf_hi(h0) + bf_hi(r0);
+        s[b][2] = bf_lo(h1) + bf_lo(r1); s[b][3] = bf_hi(h1) + bf_hi(r1);
+      }
     }
   }
-  if (res_out != TW_NONE && ok) {
+  // this thread's 4 features of the new residual, when this task owns them
+  if (res_out != TW_NONE && res_owner && ok) {
 #pragma unroll
     for (int b = 0; b < B; b++) {
-      uint64_t* o = c.ws.tw(res_out + (size_t)b * (H / 2) + 2 * t);
-      st_co(o, tw_make(f2bf(s[b][0]) | (f2bf(s[b][1]) << 16), tag_out));
-      st_co(o + 1, tw_make(f2bf(s[b][2]) | (f2bf(s[b][3]) << 16), tag_out));
+      const size_t o = res_out + (size_t)b * (H / 2) + 2 * t;
+      st_all(c.ws, o, tw_make(f2bf(s[b][0]) | (f2bf(s[b][1]) << 16), tag_out));
+      st_all(c.ws, o + 1, tw_make(f2bf(s[b][2]) | (f2bf(s[b][3]) << 16), tag_out));
     }
   }
 #pragma unroll
@@ -300,42 +352,67 @@ __device__ __forceinline__ int p4_chunks(const Inst& w) {
   return (rows + rpc - 1) / rpc;
 }
 
+// The new residual is published by the tasks of the stage that computes it,
+// each the 4-feature slices of the threads whose index maps into its row range
+// (QKV: 16 rows per thread index, GATEUP: 12 channels), so every slice has
+// exactly one writer and no task carries the whole vector's stores.
 template <int B>
 __device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, const Inst& w) {
   const int layer = w.layer;
   const uint32_t tag = p4_tag(c.epoch, layer);
+  const int t = p4_tid();
   switch (w.op) {
     case MKD_OP_QKV: {
-      const size_t out = w.a0 == 0 ? TW_RES1 : TW_NONE;
+      const bool own = w.a0 <= QKV_N / 256 * t && QKV_N / 256 * t < w.a0 + w.a1;
       const uint16_t* nw = p4_wptr(d, layer, MKD_W_LN_IN);
-      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, out, tag);
-      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, out, tag);
+      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, TW_RES1, tag, own);
+      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, TW_RES1, tag, own);
     }
-    case MKD_OP_GATEUP:
-      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST),
-                              w.a0 == 0 ? TW_RES2 : TW_NONE, tag);
+    case MKD_OP_GATEUP: {
+      const bool own = w.a0 <= I / 256 * t && I / 256 * t < w.a0 + w.a1;
+      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST), TW_RES2, tag, own);
+    }
     case MKD_OP_OPROJ: return p4_stage_copy<B, QS>(c, TW_ATTN, tag);
     case MKD_OP_DOWN: return p4_stage_copy<B, I>(c, TW_ACT, tag);
     case MKD_OP_LMHEAD:
       return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, d.num_layers - 1), d.final_norm,
-                              TW_NONE, 0);
+                              TW_NONE, 0, false);
     default: return true;
   }
 }
 
-// The chunk loop of one GEMV task: one barrier per chunk hands the next LDS
-// slot over from the DMA waves; the op is fixed for the whole loop.
+// Chunks are handed from the DMA waves to the compute waves in groups of G
+// consecutive chunks (counted over the whole instruction row), one barrier per
+// group: the chunks of a layer task are usually one group that landed during
+// the task's dependency wait, so the task runs without a per-chunk hand-over.
+// 2G <= NS: while the compute waves read group g, the DMA waves can already
+// hold group g + 1 in the remaining slots.
+template <int NS>
+struct P4G {
+  static constexpr int G = NS / 2 < 4 ? NS / 2 : 4;
+};
+
+// The chunk loop of one GEMV task (the op is fixed for the whole loop).
 // out(i, j, acc): result i of chunk j (see chunk_gemv4 for i).
 template <int B, int K, int NS, class Out>
 __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int rows, bool aborted, uint64_t* tr,
-                                          const uint16_t* xs, Out out) {
+                                          const uint16_t* xs, Out out, uint64_t* dbg_chunks = nullptr) {
+  (void)dbg_chunks;
   constexpr int RPC = K == 1024 ? 8 : (K == 2048 ? 4 : 2);
   uint8_t* slot = ring + (cc % NS) * SLOT_BYTES;
   uint8_t* const ring_end = ring + NS * SLOT_BYTES;
   for (int j = 0; j < nch; j++) {
-    raw_barrier();
+    if ((cc + j) % P4G<NS>::G == 0) raw_barrier();  // group of G chunks handed over
     if (j == 0 && tr != nullptr && threadIdx.x == 0) tr[2] = wall_clock64();
+#ifdef MKD_TRACE_CHUNKS
+    // debug: chunk release and compute-end times after the task trace ([grid][512][2])
+    uint64_t* ct = dbg_chunks == nullptr ? nullptr : dbg_chunks + ((size_t)blockIdx.x * 512 + ((cc + j) & 511)) * 2;
+    if (ct != nullptr && threadIdx.x == 0) ct[0] = wall_clock64();
+#endif
     if (!aborted) chunk_gemv4<B, K>(slot, min(RPC, rows - j * RPC), xs, [&](int i, const float* acc) { out(i, j, acc); });
+#ifdef MKD_TRACE_CHUNKS
+    if (ct != nullptr && threadIdx.x == 0) ct[1] = wall_clock64();
+#endif
     slot += SLOT_BYTES;
     if (slot == ring_end) slot = ring;
   }
@@ -356,7 +433,8 @@ struct LmArg {
 // All chunks of GEMV task w (results into the tile; LM: argmax into best).
 template <int B, int NS>
 __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c, const Inst& w, uint8_t* ring, int cc,
-                                               int nch, bool aborted, uint64_t* tr, LmArg<B>& best) {
+                                               int nch, bool aborted, uint64_t* tr, LmArg<B>& best,
+                                               uint64_t* dbg = nullptr) {
   const int lane = threadIdx.x & 63;
   const int rows = p4_rows(w);
   float* res = c.res;
@@ -367,10 +445,10 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
   };
   switch (w.op) {
     case MKD_OP_QKV:
-    case MKD_OP_GATEUP: p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(8, 1)); break;
-    case MKD_OP_OPROJ: p4_chunks<B, QS, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(4, 1)); break;
+    case MKD_OP_GATEUP: p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(8, 1), dbg); break;
+    case MKD_OP_OPROJ: p4_chunks<B, QS, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(4, 1), dbg); break;
     // DOWN: two half-row partials per row, result tile entries 2 * row + half
-    case MKD_OP_DOWN: p4_chunks<B, I, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(2, 2)); break;
+    case MKD_OP_DOWN: p4_chunks<B, I, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(2, 2), dbg); break;
     case MKD_OP_LMHEAD: {
       uint16_t* logits = d.out_logits;
       const int a0 = w.a0;
@@ -385,7 +463,7 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
         }
         if (logits != nullptr && lane < B && lane < d.rows)
           logits[(size_t)lane * V + row] = (uint16_t)f2bf(pick_lane<B>(acc, lane));
-      });
+      }, dbg);
       break;
     }
     default: break;
@@ -394,14 +472,25 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
 
 // Publish a GEMV task's rows (bf16 pairs with the layer tag).
 template <int B>
-__device__ __forceinline__ void p4_store(const P4& c, const Inst& w) {
+__device__ __forceinline__ void p4_store(const P4& c, const Inst& w, uint64_t* dbg_st = nullptr) {
+  (void)dbg_st;
+#ifdef MKD_TRACE_CHUNKS
+  if (dbg_st != nullptr && (threadIdx.x & 63) == 0) dbg_st[threadIdx.x >> 6] = wall_clock64();
+#endif
   c.sync();  // the result tile is complete
+#ifdef MKD_TRACE_CHUNKS
+  if (dbg_st != nullptr && (threadIdx.x & 63) == 0) dbg_st[4 + (threadIdx.x >> 6)] = wall_clock64();
+#endif
   const uint32_t tag = p4_tag(c.epoch, w.layer);
   const int t = p4_tid();
   const int a0 = w.a0;
+  // store f goes to wave f % 4: on this target vmcnt also counts stores, so a
+  // wave with write-through stores in flight waits for their acknowledgement at
+  // its next load; spreading them keeps any one wave from lagging the others
+  const int fo = (t & 63) * PK_CW + (t >> 6);
   if (w.op == MKD_OP_GATEUP) {
     const int wpb = w.a1 / 2;  // channel pairs
-    for (int f = t; f < B * wpb; f += PK_CW * 64) {
+    for (int f = fo; f < B * wpb; f += PK_CW * 64) {
       const int b = f / wpb, i = f - b * wpb;
       uint32_t h[2];
 #pragma unroll
@@ -411,7 +500,7 @@ __device__ __forceinline__ void p4_store(const P4& c, const Inst& w) {
         const float u = round_bf(c.res[(2 * ch + 1) * MAXB + b]);
         h[e] = f2bf(g / (1.0f + expf(-g)) * u);
       }
-      st_co(c.ws.tw(TW_ACT + (size_t)b * (I / 2) + a0 / 2 + i), tw_make(h[0] | (h[1] << 16), tag));
+      st_all(c.ws, TW_ACT + (size_t)b * (I / 2) + a0 / 2 + i, tw_make(h[0] | (h[1] << 16), tag));
     }
     return;
   }
@@ -420,8 +509,12 @@ __device__ __forceinline__ void p4_store(const P4& c, const Inst& w) {
   else if (w.op == MKD_OP_OPROJ) { base = TW_O; stride = H / 2; }
   else { base = TW_DOWN; stride = H / 2; }
   const bool halves = w.op == MKD_OP_DOWN;  // DOWN rows arrive as two half-row partials
+  // QKV words are read only by the attention tasks of their KV head, which the
+  // schedule places on XCD (head % 8); on that XCD they can stay in L2
+  const int qkv_head = a0 < QS ? a0 / (GROUP * HD) : (a0 < QS + KVS ? (a0 - QS) / HD : (a0 - QS - KVS) / HD);
+  const bool local = w.op == MKD_OP_QKV && c.xcc == qkv_head % TW_NREP;
   const int wpb = w.a1 / 2;
-  for (int f = t; f < B * wpb; f += PK_CW * 64) {
+  for (int f = fo; f < B * wpb; f += PK_CW * 64) {
     const int b = f / wpb, i = f - b * wpb;
     float v0, v1;
     if (halves) {
@@ -432,7 +525,10 @@ __device__ __forceinline__ void p4_store(const P4& c, const Inst& w) {
       v1 = c.res[(2 * i + 1) * MAXB + b];
     }
     const uint32_t lo = f2bf(v0), hi = f2bf(v1);
-    st_co(c.ws.tw(base + (size_t)b * stride + a0 / 2 + i), tw_make(lo | (hi << 16), tag));
+    const size_t word = base + (size_t)b * stride + a0 / 2 + i;
+    if (w.op != MKD_OP_QKV) st_all(c.ws, word, tw_make(lo | (hi << 16), tag));
+    else if (local) st_local(c.ws.tw(word), tw_make(lo | (hi << 16), tag));
+    else st_co(c.ws.tw(word), tw_make(lo | (hi << 16), tag));
   }
 }
 
@@ -501,16 +597,57 @@ __device__ __forceinline__ float xor16_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Cache row of position p in the row's block table (block clamped into the cache).
+__device__ __forceinline__ size_t attn_slot(cint32_t* table, int bs, int nblk, int p) {
+  return (size_t)min(max(table[p / bs], 0), nblk - 1) * bs + p % bs;
+}
+// Cached K/V of the sub-tile t0 .. t0 + 15 (positions >= c_end repeat t0):
+// K in the scores layout (lane: position pl, dims 32 quarter ..), V in the P*V
+// layout (lane: positions 4 pg + i, dims dg ..). With bs a multiple of 16 the
+// sub-tile lies in one block: one wave-uniform table lookup.
+__device__ __forceinline__ void attn_load_subtile(uint4 (&kreg)[4], uint4 (&vreg)[4], const uint16_t* kbase,
+                                                  const uint16_t* vbase, cint32_t* table, int bs, int nblk, int t0,
+                                                  int c_end, int pl, int quarter, int pg, int dg) {
+  const int pk = t0 + pl < c_end ? t0 + pl : t0;
+  size_t rowk, rowv[4];
+  if (bs % 16 == 0) {
+    const size_t base = (size_t)min(max(table[t0 / bs], 0), nblk - 1) * bs - (size_t)(t0 / bs) * bs;
+    rowk = base + pk;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int pv = t0 + 4 * pg + i < c_end ? t0 + 4 * pg + i : t0;
+      rowv[i] = base + pv;
+    }
+  } else {
+    rowk = attn_slot(table, bs, nblk, pk);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int pv = t0 + 4 * pg + i < c_end ? t0 + 4 * pg + i : t0;
+      rowv[i] = attn_slot(table, bs, nblk, pv);
+    }
+  }
+  const uint4* krow = reinterpret_cast<const uint4*>(kbase + rowk * KVS + quarter * 32);
+#pragma unroll
+  for (int i = 0; i < 4; i++) kreg[i] = krow[i];
+#pragma unroll
+  for (int i = 0; i < 4; i++) vreg[i] = *reinterpret_cast<const uint4*>(vbase + rowv[i] * KVS + dg);
+}
+
 // ATTN task (row b, KV head h, split of nsplit of the row's positions).
 // Everything that does not depend on this step's q/k/v is requested before
 // its words are polled: the row's position and pages, the q/k norm weights,
-// the RoPE row and the split's first tile of cached K/V (64 positions per
-// wave). After the poll: q/k RMSNorm + RoPE in registers, the new token's K/V
-// written to its cache slot (split 0 of an active row) straight from
-// registers, scores (lane = position), softmax, P*V with the probabilities
-// broadcast through LDS (lane = 8 dims x 1 of 4 position groups), the four
-// position groups summed with permlane swaps, the four waves merged in LDS.
-// The last split folds in the other splits' tagged partials.
+// the RoPE row and the first cached K/V of each wave. After the poll: q/k
+// RMSNorm + RoPE in registers, the new token's K/V written to its cache slot
+// (split 0 of an active row) straight from registers, then online softmax over
+// the split's cached positions in sub-tiles of 16 positions, one per wave and
+// round (positions p_begin + 16 w + 64 r):
+//   scores: lane (position p = lane & 15, dim quarter lane >> 4) dots 32 dims
+//           of K with both q heads; the quarters are summed with permlane swaps;
+//   P * V:  lane (8 dims (lane & 15) * 8, 4 positions 4 (lane >> 4) + i), with
+//           the 16 probabilities passed through LDS.
+// The four position groups and the four waves are merged at the end; the
+// token's own K/V (not yet in the cache when this task reads it) comes from
+// registers. The last split folds in the other splits' tagged partials.
 template <int B>
 __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int bh, int split, int nsplit,
                                         uint64_t* tr) {
@@ -520,7 +657,6 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   const int t = p4_tid(), wave = t >> 6, lane = t & 63;
   const uint32_t tag = p4_tag(c.epoch, layer);
   const int b = bh / NKV, h = bh % NKV;
-  // row state through scalar loads (b is wave-uniform)
   bool live = b < d.rows;
   int pos = live ? as_const(d.cache_seqlens)[b] : 0;
   const int bs = d.block_size;
@@ -538,49 +674,31 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   uint16_t* vb = kb + HD;                                 // [128] v
   float* mrg = reinterpret_cast<float*>(smem + 1024);     // [4 waves][2][128]
   float* mrg_ml = mrg + PK_CW * GROUP * HD;               // [4][2] m, [4][2] l
-  float* pb = reinterpret_cast<float*>(c.xs) + wave * 128;  // [2][64] this wave's probabilities (xs is free here)
+  float* pb = reinterpret_cast<float*>(c.xs) + wave * 32; // [2][16] this wave's probabilities (xs is free here)
 
   const int ctx = pos + 1;
   const int chunk = ((ctx + nsplit - 1) / nsplit + 63) & ~63;
   const int p_begin = split * chunk;
   const int p_end = min(ctx, p_begin + chunk);
   const int c_end = min(p_end, pos);  // cached positions of this split
-  const int dg = (lane & 15) * 8, sub = lane >> 4;
+  const int pl = lane & 15, quarter = lane >> 4;   // scores: position, dim quarter
+  const int dg = (lane & 15) * 8, pg = lane >> 4;  // P*V: dims, position group
   const size_t layer_off = (size_t)layer * (size_t)d.kv_layer_stride + (size_t)h * HD;
   const uint16_t* kbase = d.k_cache + layer_off;
   const uint16_t* vbase = d.v_cache + layer_off;
-  // physical block of position p (clamped into the cache)
-  auto block_of = [&](int p) { return min(max(table[p / bs], 0), nblk - 1); };
-  uint4 kreg[HD / 8], vreg[16];
-  auto load_tile = [&](int t0) {
-    if (bs % 64 == 0) {
-      // a 64-aligned tile lies in one block: one scalar lookup
-      const size_t blk_base = (size_t)block_of(t0) * bs - (t0 / bs) * bs;
-      const int p = t0 + lane < c_end ? t0 + lane : t0;
-      const uint4* krow = reinterpret_cast<const uint4*>(kbase + (blk_base + p) * KVS);
-#pragma unroll
-      for (int i = 0; i < HD / 8; i++) kreg[i] = krow[i];
-#pragma unroll
-      for (int it = 0; it < 16; it++) {
-        int pp = t0 + 4 * it + sub;
-        pp = pp < c_end ? pp : t0;
-        vreg[it] = *reinterpret_cast<const uint4*>(vbase + (blk_base + pp) * KVS + dg);
-      }
-    } else {
-      const int p = t0 + lane < c_end ? t0 + lane : t0;
-      const uint4* krow = reinterpret_cast<const uint4*>(kbase + ((size_t)block_of(p) * bs + p % bs) * KVS);
-#pragma unroll
-      for (int i = 0; i < HD / 8; i++) kreg[i] = krow[i];
-#pragma unroll
-      for (int it = 0; it < 16; it++) {
-        int pp = t0 + 4 * it + sub;
-        pp = pp < c_end ? pp : t0;
-        vreg[it] = *reinterpret_cast<const uint4*>(vbase + ((size_t)block_of(pp) * bs + pp % bs) * KVS + dg);
-      }
-    }
-  };
-  const int first_t0 = p_begin + wave * 64;
-  if (first_t0 < c_end) load_tile(first_t0);
+  uint4 kreg[4], vreg[4];
+  // this step's q (waves 0, 1: heads 2h, 2h+1), k (wave 2), v (wave 3): one word per
+  // lane; its first poll load goes out before every other load of the task
+  size_t src;
+  if (wave < 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + (size_t)(GROUP * h + wave) * (HD / 2) + lane;
+  else if (wave == 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + QS / 2 + (size_t)h * (HD / 2) + lane;
+  else src = TW_QKV + (size_t)b * (QKV_N / 2) + (QS + KVS) / 2 + (size_t)h * (HD / 2) + lane;
+  auto qaddr = [=](int) { return c.ws.tw(src); };
+  uint64_t qfirst[1];
+  poll_issue<1>(qaddr, qfirst);
+  const int first_t0 = p_begin + wave * 16;
+  if (first_t0 < c_end)
+    attn_load_subtile(kreg, vreg, kbase, vbase, table, bs, nblk, first_t0, c_end, pl, quarter, pg, dg);
   // static operands of the norm/RoPE step, and the new token's cache slot
   uint32_t wnw = 0;
   float c0 = 0.f, c1 = 0.f, s0 = 0.f, s1 = 0.f;
@@ -593,13 +711,8 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   }
   const int blk_new = (split == 0 && active) ? table[pos / bs] : 0;
 
-  // this step's q (waves 0, 1: heads 2h, 2h+1), k (wave 2), v (wave 3): one word per lane
-  size_t src;
-  if (wave < 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + (size_t)(GROUP * h + wave) * (HD / 2) + lane;
-  else if (wave == 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + QS / 2 + (size_t)h * (HD / 2) + lane;
-  else src = TW_QKV + (size_t)b * (QKV_N / 2) + (QS + KVS) / 2 + (size_t)h * (HD / 2) + lane;
   uint64_t qv[1];
-  bool ok = poll_tagged<1>([&](int) { return c.ws.tw(src); }, qv, tag, c.ws);
+  bool ok = poll_finish<1>(qaddr, qfirst, qv, tag, c.ws);
   const uint32_t word = (uint32_t)qv[0];  // dims 2*lane, 2*lane + 1
   uint32_t outw = word;
   if (wave < 3) {
@@ -608,7 +721,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     const float r = 1.0f / sqrtf(ss * (1.0f / HD) + EPS);
     const float n0 = round_bf(round_bf(x0 * r) * bf_lo(wnw));
     const float n1 = round_bf(round_bf(x1 * r) * bf_hi(wnw));
-    // rotate-half RoPE pairs dims i and i + 64: lane L holds 2L, 2L+1, lane L^32 the partners
+    // rotate-half RoPE pairs dims i and i + 64: lane L holds 2L, 2L+1, lane L^32 the partners.
     // permlane32_swap(x, x) returns {[x_lo, x_lo], [x_hi, x_hi]} by 32-lane halves:
     // the value of lane L ^ 32 is the second for L < 32 and the first otherwise
     const auto sw0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(n0), __float_as_uint(n0), false, false);
@@ -635,47 +748,49 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   if (!p4_agree(c, ok)) return false;
   if (tr != nullptr && t == 0) tr[2] = wall_clock64();
 
+  // this lane's 32 dims of both q heads (scores layout), kept for all sub-tiles
+  uint4 qa[4], qc[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    qa[i] = reinterpret_cast<const uint4*>(qb + quarter * 32)[i];
+    qc[i] = reinterpret_cast<const uint4*>(qb + HD + quarter * 32)[i];
+  }
   float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
   float a0[8], a1[8];
 #pragma unroll
   for (int jj = 0; jj < 8; jj++) { a0[jj] = 0.f; a1[jj] = 0.f; }
-  const uint4* q0 = reinterpret_cast<const uint4*>(qb);
-  const uint4* q1 = reinterpret_cast<const uint4*>(qb + HD);
-  for (int t0 = first_t0; t0 < c_end; t0 += PK_CW * 64) {
-    asm volatile("" ::: "memory");  // keep the q reads (LDS) inside the tile
-    if (t0 != first_t0) load_tile(t0);
-    const bool valid = t0 + lane < c_end;
+  for (int t0 = first_t0; t0 < c_end; t0 += PK_CW * 16) {
+    if (t0 != first_t0) attn_load_subtile(kreg, vreg, kbase, vbase, table, bs, nblk, t0, c_end, pl, quarter, pg, dg);
     float sc0 = 0.f, sc1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < HD / 8; i++) {
-      sc0 = dot8(kreg[i], q0[i], sc0);
-      sc1 = dot8(kreg[i], q1[i], sc1);
+    for (int i = 0; i < 4; i++) {
+      sc0 = dot8(kreg[i], qa[i], sc0);
+      sc1 = dot8(kreg[i], qc[i], sc1);
     }
+    sc0 = xor32_sum(xor16_sum(sc0));  // full 128-dim scores, replicated over the quarters
+    sc1 = xor32_sum(xor16_sum(sc1));
+    const bool valid = t0 + pl < c_end;
     sc0 = valid ? sc0 * ATTN_SCALE : -INFINITY;
     sc1 = valid ? sc1 * ATTN_SCALE : -INFINITY;
     const float n0 = fmaxf(m0, wave_max(sc0)), n1 = fmaxf(m1, wave_max(sc1));
     const float al0 = expf(m0 - n0), al1 = expf(m1 - n1);
     const float e0 = expf(sc0 - n0), e1 = expf(sc1 - n1);
-    l0 = l0 * al0 + wave_sum(e0);
-    l1 = l1 * al1 + wave_sum(e1);
+    // each position's probability is replicated 4 times over the wave
+    l0 = l0 * al0 + 0.25f * wave_sum(e0);
+    l1 = l1 * al1 + 0.25f * wave_sum(e1);
     m0 = n0; m1 = n1;
-    // probabilities to LDS, position p = 4 * it + sub at [sub][it]: lane (dg, sub) reads 16 in a row
-    pb[(lane & 3) * 16 + (lane >> 2)] = e0;
-    pb[64 + (lane & 3) * 16 + (lane >> 2)] = e1;
+    if (lane < 16) { pb[lane] = e0; pb[16 + lane] = e1; }
+    const float4 x = reinterpret_cast<const float4*>(pb)[pg];
+    const float4 y = reinterpret_cast<const float4*>(pb + 16)[pg];
+    const float w0[4] = {x.x, x.y, x.z, x.w}, w1[4] = {y.x, y.y, y.z, y.w};
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) { a0[jj] *= al0; a1[jj] *= al1; }
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const float4 x = reinterpret_cast<const float4*>(pb + sub * 16)[q];
-      const float4 y = reinterpret_cast<const float4*>(pb + 64 + sub * 16)[q];
-      const float w0[4] = {x.x, x.y, x.z, x.w}, w1[4] = {y.x, y.y, y.z, y.w};
+    for (int e = 0; e < 4; e++) {
+      const uint4 v = vreg[e];
+      const float vf[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const uint4 v = vreg[4 * q + e];
-        const float vf[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
-#pragma unroll
-        for (int jj = 0; jj < 8; jj++) { a0[jj] += w0[e] * vf[jj]; a1[jj] += w1[e] * vf[jj]; }
-      }
+      for (int jj = 0; jj < 8; jj++) { a0[jj] += w0[e] * vf[jj]; a1[jj] += w1[e] * vf[jj]; }
     }
   }
   if (wave == 0 && p_begin <= pos && pos < p_end) {
@@ -692,8 +807,8 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     const float vf[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) {
-      a0[jj] = a0[jj] * al0 + (sub == 0 ? e0 * vf[jj] : 0.f);
-      a1[jj] = a1[jj] * al1 + (sub == 0 ? e1 * vf[jj] : 0.f);
+      a0[jj] = a0[jj] * al0 + (pg == 0 ? e0 * vf[jj] : 0.f);
+      a1[jj] = a1[jj] * al1 + (pg == 0 ? e1 * vf[jj] : 0.f);
     }
   }
   // sum the four position groups (rows of 16 lanes), then merge the waves in LDS
@@ -730,11 +845,14 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   if (nsplit > 1) {
     const size_t pbase = TW_APART + (((size_t)b * NKV + h) * MAXS) * PART_STRIDE;
     if (split != nsplit - 1) {
+      // read only by the last split of this (row, head), placed on the same XCD
       uint64_t* part = c.ws.tw(pbase + (size_t)split * PART_STRIDE);
-      st_co(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
+      const bool local = c.xcc == h % TW_NREP;
+      auto put = [&](uint64_t* q, uint64_t v) { if (local) st_local(q, v); else st_co(q, v); };
+      put(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
       if (dd == 0) {
-        st_co(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
-        st_co(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
+        put(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
+        put(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
       }
       c.sync();  // the scratch is reused by this workgroup's next task
       return true;
@@ -761,7 +879,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   const uint32_t mine = f2bf(num / den);
   const uint32_t nbr = __shfl_xor(mine, 1, 64);
   if ((dd & 1) == 0)
-    st_co(c.ws.tw(TW_ATTN + (size_t)b * (QS / 2) + ((GROUP * h + g) * HD + dd) / 2), tw_make(mine | (nbr << 16), tag));
+    st_all(c.ws, TW_ATTN + (size_t)b * (QS / 2) + ((GROUP * h + g) * HD + dd) / 2, tw_make(mine | (nbr << 16), tag));
   return p4_agree(c, ok);  // also frees the scratch for the next task
 }
 
@@ -906,18 +1024,41 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
   const int n = __builtin_amdgcn_readfirstlane(n_inst_arg);
   uint8_t* ring = uniform_ptr(ring_arg);
   const int dw = __builtin_amdgcn_readfirstlane(dw_arg);
-  (void)ws_arg;  // workspace base (debug hooks)
-  int ti = 0, tj = 0, issued = 0;
-  DmaTask cur{};
-  auto next_task = [&]() {
-    for (; ti < n; ti++) {
-      cur = dma_decode(lp, emb, load_inst(crow + ti * MKD_INST_WORDS), dw);
-      if (cur.nch > 0) return;
+#ifdef MKD_TRACE_CHUNKS
+  // debug: chunk arrival/release/issue times after the compute waves' ([grid][512][3])
+  uint64_t* dbg = reinterpret_cast<uint64_t*>(uniform_ptr(ws_arg));
+#endif
+  (void)ws_arg;
+  // Task decode is software-pipelined: the instruction words of the task after
+  // `nxt` and the weight pointers of `nxt` are requested (scalar loads) while
+  // `cur` is being issued, so no chunk hand-over waits on a scalar-cache miss.
+  int pf = 0;  // index of the prefetched instruction in `pinst`
+  Inst pinst{};
+  if (n > 0) pinst = load_inst(crow);
+  auto next_weight_task = [&]() {
+    while (pf < n) {
+      const Inst w = pinst;
+      pf++;
+      if (pf < n) pinst = load_inst(crow + pf * MKD_INST_WORDS);
+      const DmaTask t = dma_decode(lp, emb, w, dw);
+      if (t.nch > 0) return t;
     }
-    cur.nch = 0;
+    DmaTask none{};
+    none.nch = 0;
+    return none;
   };
+  // make every field of t wave-resident now (waits for its scalar loads here,
+  // before newer scalar loads are issued behind them)
+  auto settle = [](const DmaTask& t) {
+    asm volatile("" ::"s"(t.kind), "s"(t.nch), "s"(t.nfull), "s"(t.units), "s"(t.stride), "s"(t.b0), "s"(t.b1),
+                 "s"(t.src), "s"(t.kstep), "s"(t.cstep), "s"(t.lds0), "s"(t.ldsk));
+  };
+  constexpr int G = P4G<Cfg::NS>::G;
+  int tj = 0, issued = 0;
+  DmaTask cur = next_weight_task();
+  settle(cur);
+  DmaTask nxt = next_weight_task();
   auto issue_one = [&]() {
-    if (cur.nch == 0) return;
     uint8_t* slot = ring + (issued % Cfg::NS) * SLOT_BYTES;
     if (cur.kind == 0) dma_issue<H>(cur, tj, slot, dw);
     else if (cur.kind == 1) dma_issue<QS>(cur, tj, slot, dw);
@@ -925,16 +1066,20 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
     issued++;
     if (++tj == cur.nch) {
       tj = 0;
-      ti++;
-      next_task();
+      cur = nxt;
+      settle(cur);
+      nxt = next_weight_task();
     }
   };
-  next_task();
-  for (int k = 0; k < Cfg::D; k++) issue_one();
-  for (int r = 0; r < issued; r++) {
-    wait_chunk<Cfg::D - 1>(issued - r - 1);
+  // before the first hand-over no slot is in use: fill the ring
+  while (cur.nch > 0 && issued < Cfg::NS) issue_one();
+  // group g = chunks [g G, g G + G): after its hand-over the compute waves are
+  // done with group g - 1, so chunks up to g G + NS - 1 may be issued
+  for (int g = 0; g * G < issued; g++) {
+    const int e = min(g * G + G, issued);   // end of group g (issued >= e: 2G <= NS)
+    wait_chunk<Cfg::NS - 1>(issued - e);     // chunk e - 1 (and all before) landed
     raw_barrier();
-    issue_one();
+    while (cur.nch > 0 && issued < g * G + Cfg::NS) issue_one();
   }
 }
 
@@ -957,10 +1102,16 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
   }
   __syncthreads();
   if (wave >= PK_CW) {
-    p4_dma<B>(d.layer_ptrs, d.embed, row, n_inst, ring, wave - PK_CW, reinterpret_cast<uint8_t*>(d.workspace));
+#ifdef MKD_TRACE_CHUNKS
+    uint8_t* dbg_dw = d.trace == nullptr ? nullptr
+                                         : reinterpret_cast<uint8_t*>(d.trace + (size_t)s.grid * s.max_inst * 4 + 256 * 512 * 2);
+#else
+    uint8_t* dbg_dw = nullptr;
+#endif
+    p4_dma<B>(d.layer_ptrs, d.embed, row, n_inst, ring, wave - PK_CW, dbg_dw);
     return;
   }
-  const P4 c{ws, (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch)}, flags,
+  const P4 c{ws, (int)(blockIdx.x % TW_NREP), p4_xcc_id(), (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch)}, flags,
              reinterpret_cast<float*>(scratch + P4_SCR_RED), reinterpret_cast<float*>(scratch + P4_SCR_RES), xs,
              scratch + P4_SCR_ATTN};
   bool aborted = false;
@@ -987,11 +1138,25 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
     if (tr != nullptr && threadIdx.x == 0) tr[1] = wall_clock64();
     LmArg<B> best;
     best.reset();
-    p4_task_chunks<B, Cfg::NS>(d, c, w, ring, cc, nch, aborted, tr, best);
+#ifdef MKD_TRACE_CHUNKS
+    uint64_t* dbg = d.trace == nullptr ? nullptr : d.trace + (size_t)s.grid * s.max_inst * 4;
+#else
+    uint64_t* dbg = nullptr;
+#endif
+    p4_task_chunks<B, Cfg::NS>(d, c, w, ring, cc, nch, aborted, tr, best, dbg);
     cc += nch;
     if (!aborted) {
       if (w.op == MKD_OP_LMHEAD) aborted = !p4_lm_finish<B>(d, c, w, best);
-      else p4_store<B>(c, w);
+      else {
+#ifdef MKD_TRACE_CHUNKS
+        uint64_t* dbg_st = d.trace == nullptr ? nullptr
+                                              : d.trace + (size_t)s.grid * s.max_inst * 4 + 256 * 512 * 5 +
+                                                    ((size_t)blockIdx.x * s.max_inst + i) * 8;
+#else
+        uint64_t* dbg_st = nullptr;
+#endif
+        p4_store<B>(c, w, dbg_st);
+      }
     }
     if (tr != nullptr && threadIdx.x == 0) tr[3] = wall_clock64();
   }

@@ -18,6 +18,7 @@ MAX_SPLITS = 16
 INST_WORDS = 8
 MAX_LM_SLOTS = 1024
 LAYER_PTRS = 11
+TW_REPLICAS = 8          # replicas of the tagged buffers every workgroup reads (one per XCD)
 
 FLAG_ADVANCE = 1
 FLAG_ZERO_FANIN = 2
@@ -184,13 +185,16 @@ def workspace_layout() -> dict[str, tuple[int, int]]:
     ctr_lines = 3 + layers * maxb * kv_heads + layers * (kv_heads + 4) * 8
     out["counters"] = (off, 128 * ctr_lines)
     off = (off + 128 * ctr_lines + 255) & ~255
-    words = [
-        ("tw_res1", maxb * h // 2), ("tw_res2", maxb * h // 2), ("tw_qkv", maxb * qkv // 2),
-        ("tw_attn", maxb * qs // 2), ("tw_o", maxb * h // 2), ("tw_act", maxb * i // 2),
-        ("tw_down", maxb * h // 2), ("tw_apart", maxb * kv_heads * MAX_SPLITS * part_stride),
-        ("tw_lm", MAX_LM_SLOTS * maxb * 2),
-    ]
-    for name, n in words:
+    group = [("tw_res1", maxb * h // 2), ("tw_res2", maxb * h // 2), ("tw_attn", maxb * qs // 2),
+             ("tw_o", maxb * h // 2), ("tw_act", maxb * i // 2), ("tw_down", maxb * h // 2)]
+    group_words = sum(n for _, n in group)
+    for name, n in group:      # replica 0 of the replicated buffers
+        out[name] = (off, 8 * n)
+        off += 8 * n
+    out["tw_replica_stride"] = (8 * group_words, 0)
+    off += 8 * group_words * (TW_REPLICAS - 1)
+    for name, n in [("tw_qkv", maxb * qkv // 2), ("tw_apart", maxb * kv_heads * MAX_SPLITS * part_stride),
+                    ("tw_lm", MAX_LM_SLOTS * maxb * 2)]:
         out[name] = (off, 8 * n)
         off += 8 * n
     out["end"] = (off, 0)

@@ -253,10 +253,51 @@ def place_round_robin(stages: list[Stage], num_wgs: int) -> list[list[Task]]:
     return rows
 
 
+XCDS = 8  # accelerator dies of an MI355X; workgroup w of a launch runs on die w % 8
+
+
+def task_kv_head(t: Task) -> int:
+    """KV head whose rows a QKV task computes, or whose attention an ATTN task runs."""
+
+    if t.op == OP_ATTN:
+        return t.a0 % NUM_KV_HEADS
+    r = t.a0
+    if r < Q_SIZE:
+        return r // (2 * HEAD_DIM)
+    if r < Q_SIZE + KV_SIZE:
+        return (r - Q_SIZE) // HEAD_DIM
+    return (r - Q_SIZE - KV_SIZE) // HEAD_DIM
+
+
+def place_xcd_aware(stages: list[Stage], num_wgs: int) -> list[list[Task]]:
+    """Round-robin placement, except that the QKV and attention tasks of KV head
+    ``h`` go to the workgroups of die ``h % 8`` (w % 8 == h % 8): their exchange
+    (and the split-KV merge) then stays in that die's L2. Rows stay in stage order.
+    Falls back to plain round-robin when the grid is not a multiple of 8."""
+
+    if num_wgs % XCDS:
+        return place_round_robin(stages, num_wgs)
+    rows: list[list[Task]] = [[] for _ in range(num_wgs)]
+    per_die = num_wgs // XCDS
+    cursor = 0
+    head_cursor = [0] * NUM_KV_HEADS
+    for st in stages:
+        if st.op in (OP_QKV, OP_ATTN):
+            for t in st.tasks:
+                h = task_kv_head(t)
+                rows[h % XCDS + XCDS * (head_cursor[h] % per_die)].append(t)
+                head_cursor[h] += 1
+        else:
+            for t in st.tasks:
+                rows[cursor].append(t)
+                cursor = (cursor + 1) % num_wgs
+    return rows
+
+
 def build_schedule(batch: int, attn_splits: int, num_wgs: int,
                    num_layers: int = NUM_LAYERS) -> Schedule:
     stages = build_stages(batch, attn_splits, num_wgs, num_layers)
-    rows = place_round_robin(stages, num_wgs)
+    rows = place_xcd_aware(stages, num_wgs)
     return Schedule(batch=batch, attn_splits=attn_splits, num_layers=num_layers,
                     grid=num_wgs, stages=stages, rows=rows)
 
@@ -282,5 +323,5 @@ def build_segments(batch: int, attn_splits: int, num_wgs: int, num_layers: int =
     for start, end in split_layers(num_layers, groups):
         seg = [s for s in stages if start <= s.layer < end or (end == num_layers and s.op == OP_LMHEAD)]
         out.append(Schedule(batch=batch, attn_splits=attn_splits, num_layers=num_layers,
-                            grid=num_wgs, stages=seg, rows=place_round_robin(seg, num_wgs)))
+                            grid=num_wgs, stages=seg, rows=place_xcd_aware(seg, num_wgs)))
     return out

@@ -106,3 +106,17 @@ def test_tagged_exchange_preconditions_at_256_cus(batch, splits):
     from nanovllm.backends.megakernel.taskgraph import _check_tagged_preconditions
     for groups in (1, 4):
         _check_tagged_preconditions(build_segments(batch, splits, 256, 28, groups))
+
+
+def test_xcd_aware_placement_keeps_heads_on_their_die():
+    """QKV and attention tasks of KV head h sit on workgroups w with w % 8 == h % 8;
+    every workgroup still gets one LM task and the schedule still verifies."""
+    from nanovllm.backends.megakernel.schedule import task_kv_head
+    for batch, splits in ((1, 1), (8, 4)):
+        s = build_schedule(batch, splits, 256, 28)
+        assert verify(s) == []
+        for w, row in enumerate(s.rows):
+            for t in row:
+                if t.op in (native.OP_QKV, native.OP_ATTN):
+                    assert task_kv_head(t) % 8 == w % 8
+            assert sum(t.op == native.OP_LMHEAD for t in row) == 1
