@@ -36,9 +36,13 @@ namespace mkd {
 constexpr int P4_MAX_ROWS = 32;      // rows of one GEMV task held in the result tile
 constexpr int P4_SCR_FLAGS = 64;     // int [0] abort, [1] epoch
 constexpr int P4_SCR_RED = 128;      // float [4][MAXB] sums / LM (value, index)
+constexpr int P4_SCR_STAGE = 512;   // u32 [2 parities][2 owners][MAXB][2] residual words awaiting publication
+constexpr int P4_STAGE_WORDS = 2 * MAXB * 2;
 constexpr int P4_SCR_RES = 1024;     // float [P4_MAX_ROWS][MAXB] task results
 constexpr int P4_SCR_ATTN = 2048;    // attention scratch (6 KiB)
 static_assert(P4_SCR_RES + 4 * P4_MAX_ROWS * MAXB <= P4_SCR_ATTN, "result tile overlaps");
+static_assert(P4_SCR_RED + 2 * 4 * PK_CW * MAXB <= P4_SCR_STAGE && P4_SCR_STAGE + 4 * 2 * P4_STAGE_WORDS <= P4_SCR_RES,
+              "staging area overlaps");
 static_assert(P4_SCR_ATTN + 6144 <= PK_SCRATCH, "attention scratch too large");
 
 constexpr size_t TW_NONE = ~(size_t)0;
@@ -62,10 +66,28 @@ __device__ __forceinline__ int p4_xcc_id() {
 __device__ __forceinline__ void st_local(uint64_t* p, uint64_t v) {
   asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
 }
-// A word every workgroup reads: one write-through copy per XCD replica.
-__device__ __forceinline__ void st_all(const Ws& ws, size_t word, uint64_t v) {
-#pragma unroll
-  for (int r = 0; r < TW_NREP; r++) st_co(ws.tw(word + (size_t)r * TW_GROUP), v);
+// Words every workgroup reads have one write-through copy per XCD replica.
+// One replica of a word every workgroup reads. Callers spread the replicas of
+// a word over lanes: a store instruction costs the same with 1 or 64 active
+// lanes, and a wave with more than 63 stores in flight stalls its issue until
+// write-through acknowledgements (~2 us) come back.
+__device__ __forceinline__ void st_rep(const Ws& ws, size_t word, int rep, uint64_t v) {
+  st_co(ws.tw(word + (size_t)rep * TW_GROUP), v);
+}
+
+// Plain load through a global-address-space pointer. A pointer read from
+// memory is generic to the compiler, which would emit a flat load: flat loads
+// count against the LDS counter too, so every LDS wait after one also waits
+// for the global load.
+// (T a scalar type: a struct such as uint2 would be copied through a generic reference)
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+  typedef __attribute__((address_space(1))) const T global_t;
+  return *(global_t*)p;
+}
+__device__ __forceinline__ uint2 ldg2u(const void* p) {
+  const uint64_t v = ldg(reinterpret_cast<const uint64_t*>(p));
+  return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
 }
 
 __device__ __forceinline__ uint32_t p4_tag(uint32_t epoch, int layer) { return (epoch + 1u) * 32u + (uint32_t)layer; }
@@ -103,7 +125,37 @@ struct P4 {
   float* res;
   uint16_t* xs;
   uint8_t* attn_smem;
+  uint32_t* stage;  // [2][P4_STAGE_WORDS] residual words of a task's owners, [owner][b][2]
+  int par;          // staging buffer of the current task, alternating over the tasks that
+                    // stage (QKV, GATEUP): a task reads its buffer after its last barrier,
+                    // and the next task to write that buffer comes after another staging
+                    // task, behind that task's barriers.
+  uint64_t* trp;    // this task's trace record (debug builds with MKD_TRACE_POLL)
 };
+
+#ifdef MKD_TRACE_POLL
+constexpr int P4_TR_STRIDE = 8;  // debug records: slots 4.. hold points inside the prologue
+#else
+constexpr int P4_TR_STRIDE = 4;
+#endif
+// Debug: wave-maximum time stamp in slot k of the task's trace record.
+__device__ __forceinline__ void p4_trace_at(const P4& c, int k) {
+#ifdef MKD_TRACE_POLL
+  if (c.trp != nullptr && (threadIdx.x & 63) == 0)
+    atomicMax(reinterpret_cast<unsigned long long*>(c.trp + k), (unsigned long long)wall_clock64());
+#else
+  (void)c; (void)k;
+#endif
+}
+// Debug: time at which the task's first dependency poll completed (trace slot 2).
+__device__ __forceinline__ void p4_trace_poll(const P4& c) {
+#ifdef MKD_TRACE_POLL
+  if (c.trp != nullptr && (threadIdx.x & 63) == 0)  // the last of the four waves
+    atomicMax(reinterpret_cast<unsigned long long*>(c.trp + 2), (unsigned long long)wall_clock64());
+#else
+  (void)c;
+#endif
+}
 
 // First round of a poll: issue the loads (returned in a[]). Issuing it before
 // a task's other loads matters: loads complete in issue order, so a check of
@@ -114,7 +166,8 @@ __device__ __forceinline__ void poll_issue(Addr addr, uint64_t (&a)[N]) {
   for (int k = 0; k < N; k++) a[k] = ld_co(addr(k));
 }
 // Check the first round and keep polling until every word carries `tag`
-// (one round in flight: measured no slower than two, with half the traffic).
+// (one round in flight: measured no slower than two, with half the traffic;
+// re-polling only one word while the others are missing measured slower).
 template <int N, class Addr>
 __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_t (&v)[N], uint32_t tag,
                                             const Ws& ws) {
@@ -122,9 +175,13 @@ __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_
   uint32_t pending = N == 32 ? ~0u : ((1u << N) - 1u);
   uint64_t t0 = 0;
   for (uint32_t spin = 0;; spin++) {
+    // Every word is examined on every round (one already seen keeps its value
+    // and tag in a[k]): a load the compiler sees unconsumed on some path makes
+    // it wait for all of the wave's memory operations before that register is
+    // next written, wherever that is.
 #pragma unroll
     for (int k = 0; k < N; k++)
-      if (((pending >> k) & 1u) && tw_tag(a[k]) == tag) { v[k] = a[k]; pending &= ~(1u << k); }
+      if (tw_tag(a[k]) == tag) { v[k] = a[k]; pending &= ~(1u << k); }
     if (pending == 0u) return true;
     if ((spin & 63u) == 0u) {
       const uint64_t now = wall_clock64();
@@ -175,6 +232,7 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
   for (int k0 = 0; k0 < PER; k0 += NB) {
     uint64_t v[NB];
     ok = ok && poll_tagged<NB>([&](int k) { return src + t + 256 * (k0 + k); }, v, tag, c.ws);
+    if (k0 == 0) p4_trace_poll(c);
 #pragma unroll
     for (int k = 0; k < NB; k++) dst[t + 256 * (k0 + k)] = (uint32_t)v[k];
   }
@@ -184,13 +242,15 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
 // Residual add + RMSNorm of B rows into xs (rounding as stage_norm in mkd_tasks.h).
 // from_embed: the rows are the embedding rows of input_ids (layer 0).
 // Otherwise s = hidden + residual from two tagged [MAXB][H/2] buffers.
-// res_out != TW_NONE: this task also publishes bf16(s) as the next residual.
+// Threads res_first .. res_first + res_n - 1 stage their 4 features of bf16(s),
+// the next residual, for p4_publish_residual at the end of the task.
 template <int B>
 __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c, bool from_embed, size_t hid,
-                                              size_t resid, uint32_t tag_in, const uint16_t* nw, size_t res_out,
-                                              uint32_t tag_out, bool res_owner) {
+                                              size_t resid, uint32_t tag_in, const uint16_t* nw, int res_first,
+                                              int res_n) {
   const int t = p4_tid(), wave = t >> 6, lane = t & 63;
   const int k0 = t * 4;  // features k0..k0+3 = words 2t, 2t+1 of each row
+  const bool res_owner = res_first <= t && t < res_first + res_n;
   float s[B][4];
   bool ok = true;
   // rows in groups of G (two rows at a time keeps the in-flight poll registers small)
@@ -203,8 +263,13 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
   };
   uint64_t first[4 * G];
   if (!from_embed) poll_issue<4 * G>(addr(0), first);    // before any other load of this task
-  const uint2 wv = *reinterpret_cast<const uint2*>(nw + k0);
+  const uint2 wv = ldg2u(nw + k0);
   if (from_embed) {
+    // first[] was not loaded on this path; consuming it here keeps the compiler
+    // from treating those loads as pending afterwards (it would then wait for
+    // every memory operation before it next writes their registers)
+#pragma unroll
+    for (int k = 0; k < 4 * G; k++) asm volatile("" ::"v"((uint32_t)first[k]));
 #pragma unroll
     for (int b = 0; b < B; b++) {
       int64_t id = b < d.rows ? d.input_ids[b] : 0;
@@ -221,6 +286,7 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
       uint64_t v[4 * G];
       if (b0 == 0) {
         ok = poll_finish<4 * G>(addr(0), first, v, tag_in, c.ws);
+        p4_trace_poll(c);
       } else {
         ok = ok && poll_tagged<4 * G>(addr(b0), v, tag_in, c.ws);
       }
@@ -234,13 +300,15 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
       }
     }
   }
-  // this thread's 4 features of the new residual, when this task owns them
-  if (res_out != TW_NONE && res_owner && ok) {
+  const float w4[4] = {bf_lo(wv.x), bf_hi(wv.x), bf_lo(wv.y), bf_hi(wv.y)};
+  // this thread's 4 features of the new residual, when this task owns them:
+  // staged in LDS as words [owner][b][2]
+  if (res_owner) {
+    uint32_t* stage = c.stage + c.par * P4_STAGE_WORDS;
 #pragma unroll
     for (int b = 0; b < B; b++) {
-      const size_t o = res_out + (size_t)b * (H / 2) + 2 * t;
-      st_all(c.ws, o, tw_make(f2bf(s[b][0]) | (f2bf(s[b][1]) << 16), tag_out));
-      st_all(c.ws, o + 1, tw_make(f2bf(s[b][2]) | (f2bf(s[b][3]) << 16), tag_out));
+      stage[((t - res_first) * B + b) * 2] = pack_bf2(s[b][0], s[b][1]);
+      stage[((t - res_first) * B + b) * 2 + 1] = pack_bf2(s[b][2], s[b][3]);
     }
   }
 #pragma unroll
@@ -249,18 +317,21 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
     ss = wave_sum(ss);
     if (lane == 0) c.red[wave * MAXB + b] = ss;
   }
+  p4_trace_at(c, 4);
   if (!p4_agree(c, ok)) return false;
-  const float w4[4] = {bf_lo(wv.x), bf_hi(wv.x), bf_lo(wv.y), bf_hi(wv.y)};
+  p4_trace_at(c, 5);
 #pragma unroll
   for (int b = 0; b < B; b++) {
     const float tot = c.red[b] + c.red[MAXB + b] + c.red[2 * MAXB + b] + c.red[3 * MAXB + b];
     const float r = 1.0f / sqrtf(tot * (1.0f / H) + EPS);
-    uint32_t o[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) o[j] = f2bf(round_bf(s[b][j] * r) * w4[j]);
-    *reinterpret_cast<uint2*>(c.xs + (size_t)b * H + k0) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+    // bf16(bf16(s * r) * w), pairwise through the packed conversion
+    const uint32_t n01 = pack_bf2(s[b][0] * r, s[b][1] * r), n23 = pack_bf2(s[b][2] * r, s[b][3] * r);
+    *reinterpret_cast<uint2*>(c.xs + (size_t)b * H + k0) =
+        make_uint2(pack_bf2(bf_lo(n01) * w4[0], bf_hi(n01) * w4[1]), pack_bf2(bf_lo(n23) * w4[2], bf_hi(n23) * w4[3]));
   }
+  p4_trace_at(c, 6);
   c.sync();
+  p4_trace_at(c, 7);
   return true;
 }
 
@@ -356,6 +427,15 @@ __device__ __forceinline__ int p4_chunks(const Inst& w) {
 // each the 4-feature slices of the threads whose index maps into its row range
 // (QKV: 16 rows per thread index, GATEUP: 12 channels), so every slice has
 // exactly one writer and no task carries the whole vector's stores.
+struct ResRange {
+  int first, n;  // owner threads first .. first + n - 1
+};
+template <int F>  // rows (channels) per thread index
+__device__ __forceinline__ ResRange p4_res_range(const Inst& w) {
+  const int first = (w.a0 + F - 1) / F;
+  return ResRange{first, (w.a0 + w.a1 + F - 1) / F - first};
+}
+
 template <int B>
 __device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, const Inst& w) {
   const int layer = w.layer;
@@ -363,20 +443,19 @@ __device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, c
   const int t = p4_tid();
   switch (w.op) {
     case MKD_OP_QKV: {
-      const bool own = w.a0 <= QKV_N / 256 * t && QKV_N / 256 * t < w.a0 + w.a1;
+      const ResRange r = p4_res_range<QKV_N / 256>(w);
       const uint16_t* nw = p4_wptr(d, layer, MKD_W_LN_IN);
-      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, TW_RES1, tag, own);
-      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, TW_RES1, tag, own);
+      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, r.first, r.n);
+      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, r.first, r.n);
     }
     case MKD_OP_GATEUP: {
-      const bool own = w.a0 <= I / 256 * t && I / 256 * t < w.a0 + w.a1;
-      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST), TW_RES2, tag, own);
+      const ResRange r = p4_res_range<I / 256>(w);
+      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST), r.first, r.n);
     }
     case MKD_OP_OPROJ: return p4_stage_copy<B, QS>(c, TW_ATTN, tag);
     case MKD_OP_DOWN: return p4_stage_copy<B, I>(c, TW_ACT, tag);
     case MKD_OP_LMHEAD:
-      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, d.num_layers - 1), d.final_norm,
-                              TW_NONE, 0, false);
+      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, d.num_layers - 1), d.final_norm, 0, 0);
     default: return true;
   }
 }
@@ -403,7 +482,9 @@ __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int ro
   uint8_t* const ring_end = ring + NS * SLOT_BYTES;
   for (int j = 0; j < nch; j++) {
     if ((cc + j) % P4G<NS>::G == 0) raw_barrier();  // group of G chunks handed over
+#ifndef MKD_TRACE_POLL
     if (j == 0 && tr != nullptr && threadIdx.x == 0) tr[2] = wall_clock64();
+#endif
 #ifdef MKD_TRACE_CHUNKS
     // debug: chunk release and compute-end times after the task trace ([grid][512][2])
     uint64_t* ct = dbg_chunks == nullptr ? nullptr : dbg_chunks + ((size_t)blockIdx.x * 512 + ((cc + j) & 511)) * 2;
@@ -470,7 +551,85 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
   }
 }
 
-// Publish a GEMV task's rows (bf16 pairs with the layer tag).
+constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
+
+// The residual words this task's owner threads staged in its prologue, one
+// store per (word, replica) spread over the waves. Issued after the task's
+// outputs: the residual is read two stages later, and stores issued before
+// the task's chunk loop would hold up the waits the compiler places there for
+// all of the wave's memory operations.
+template <int B, int F>
+__device__ __forceinline__ void p4_publish_residual(const P4& c, const Inst& w, size_t base, uint32_t tag) {
+  const ResRange r = p4_res_range<F>(w);
+  const uint32_t* stage = c.stage + c.par * P4_STAGE_WORDS;
+  const int t = p4_tid();
+  constexpr int LR = ilog2(TW_NREP), LB = ilog2(B);
+  for (int e = (t & 63) * PK_CW + (t >> 6); e < (r.n << (LB + 1 + LR)); e += PK_CW * 64) {
+    const int k = e >> LR, o = k >> (LB + 1), b = (k >> 1) & (B - 1);
+    const size_t word = base + (size_t)b * (H / 2) + 2 * (r.first + o) + (k & 1);
+    st_rep(c.ws, word, e & (TW_NREP - 1), tw_make(stage[k], tag));
+  }
+}
+
+// Publish one GEMV task's rows as tagged bf16 pairs. Entry e = (pair i, row b,
+// replica r) with r in the low bits, then b, then i, so the entries of a task
+// are the prefix e < pairs * B * replicas and all index math is shifts: this
+// epilogue sits on the step's critical path, where each instruction of a
+// single wave costs several cycles.
+template <int B, int OP>
+__device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
+  constexpr int LR = OP == MKD_OP_QKV ? 0 : ilog2(TW_NREP);  // QKV words have one reader XCD
+  constexpr int LB = ilog2(B);
+  static_assert((1 << LB) == B, "batch bucket is a power of two");
+  constexpr uint32_t STRIDE = OP == MKD_OP_QKV ? QKV_N / 2 : (OP == MKD_OP_GATEUP ? I / 2 : H / 2);
+  constexpr uint32_t BASE = OP == MKD_OP_QKV ? TW_QKV
+                            : OP == MKD_OP_OPROJ ? TW_O
+                            : OP == MKD_OP_GATEUP ? TW_ACT : TW_DOWN;
+  const uint32_t tag = p4_tag(c.epoch, w.layer);
+  const int t = p4_tid();
+  // store f goes to wave f % 4: vmcnt also counts stores, so a wave with
+  // write-through stores in flight waits for their acknowledgement at its next
+  // load; spreading them keeps any one wave from lagging the others
+  const int fo = (t & 63) * PK_CW + (t >> 6);
+  const int n = (w.a1 >> 1) << (LB + LR);  // (channel or row) pairs x rows x replicas
+  uint8_t* const twb = reinterpret_cast<uint8_t*>(c.ws.tw(BASE + (uint32_t)(w.a0 >> 1)));
+  bool local = false;
+  if (OP == MKD_OP_QKV) {
+    // read only by the attention tasks of the KV head, placed on XCD (head % 8)
+    const int a0 = w.a0;
+    const int head = a0 < QS ? a0 / (GROUP * HD) : (a0 < QS + KVS ? (a0 - QS) / HD : (a0 - QS - KVS) / HD);
+    local = c.xcc == head % TW_NREP;
+  }
+  for (int e = fo; e < n; e += PK_CW * 64) {
+    const int r = e & ((1 << LR) - 1), b = (e >> LR) & (B - 1), i = e >> (LR + LB);
+    float v0, v1;
+    if (OP == MKD_OP_GATEUP) {
+      float h[2];
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const float g = round_bf(c.res[(4 * i + 2 * k) * MAXB + b]);
+        const float u = round_bf(c.res[(4 * i + 2 * k + 1) * MAXB + b]);
+        h[k] = g / (1.0f + expf(-g)) * u;
+      }
+      v0 = h[0]; v1 = h[1];
+    } else if (OP == MKD_OP_DOWN) {  // rows arrive as two half-row partials
+      v0 = c.res[(4 * i) * MAXB + b] + c.res[(4 * i + 1) * MAXB + b];
+      v1 = c.res[(4 * i + 2) * MAXB + b] + c.res[(4 * i + 3) * MAXB + b];
+    } else {
+      v0 = c.res[(2 * i) * MAXB + b];
+      v1 = c.res[(2 * i + 1) * MAXB + b];
+    }
+    const uint64_t v = tw_make(pack_bf2(v0, v1), tag);
+    const uint32_t off = ((uint32_t)r * (uint32_t)TW_GROUP + (uint32_t)b * STRIDE + (uint32_t)i) * 8u;
+    uint64_t* q = reinterpret_cast<uint64_t*>(twb + off);
+    if (OP == MKD_OP_QKV && local) st_local(q, v);
+    else st_co(q, v);
+  }
+  if (OP == MKD_OP_QKV) p4_publish_residual<B, QKV_N / 256>(c, w, TW_RES1, tag);
+  if (OP == MKD_OP_GATEUP) p4_publish_residual<B, I / 256>(c, w, TW_RES2, tag);
+}
+static_assert(TW_WORDS * 8 < (1ull << 32), "tagged offsets are 32-bit");
+
 template <int B>
 __device__ __forceinline__ void p4_store(const P4& c, const Inst& w, uint64_t* dbg_st = nullptr) {
   (void)dbg_st;
@@ -481,54 +640,12 @@ __device__ __forceinline__ void p4_store(const P4& c, const Inst& w, uint64_t* d
 #ifdef MKD_TRACE_CHUNKS
   if (dbg_st != nullptr && (threadIdx.x & 63) == 0) dbg_st[4 + (threadIdx.x >> 6)] = wall_clock64();
 #endif
-  const uint32_t tag = p4_tag(c.epoch, w.layer);
-  const int t = p4_tid();
-  const int a0 = w.a0;
-  // store f goes to wave f % 4: on this target vmcnt also counts stores, so a
-  // wave with write-through stores in flight waits for their acknowledgement at
-  // its next load; spreading them keeps any one wave from lagging the others
-  const int fo = (t & 63) * PK_CW + (t >> 6);
-  if (w.op == MKD_OP_GATEUP) {
-    const int wpb = w.a1 / 2;  // channel pairs
-    for (int f = fo; f < B * wpb; f += PK_CW * 64) {
-      const int b = f / wpb, i = f - b * wpb;
-      uint32_t h[2];
-#pragma unroll
-      for (int e = 0; e < 2; e++) {
-        const int ch = 2 * i + e;
-        const float g = round_bf(c.res[(2 * ch) * MAXB + b]);
-        const float u = round_bf(c.res[(2 * ch + 1) * MAXB + b]);
-        h[e] = f2bf(g / (1.0f + expf(-g)) * u);
-      }
-      st_all(c.ws, TW_ACT + (size_t)b * (I / 2) + a0 / 2 + i, tw_make(h[0] | (h[1] << 16), tag));
-    }
-    return;
-  }
-  size_t base, stride;
-  if (w.op == MKD_OP_QKV) { base = TW_QKV; stride = QKV_N / 2; }
-  else if (w.op == MKD_OP_OPROJ) { base = TW_O; stride = H / 2; }
-  else { base = TW_DOWN; stride = H / 2; }
-  const bool halves = w.op == MKD_OP_DOWN;  // DOWN rows arrive as two half-row partials
-  // QKV words are read only by the attention tasks of their KV head, which the
-  // schedule places on XCD (head % 8); on that XCD they can stay in L2
-  const int qkv_head = a0 < QS ? a0 / (GROUP * HD) : (a0 < QS + KVS ? (a0 - QS) / HD : (a0 - QS - KVS) / HD);
-  const bool local = w.op == MKD_OP_QKV && c.xcc == qkv_head % TW_NREP;
-  const int wpb = w.a1 / 2;
-  for (int f = fo; f < B * wpb; f += PK_CW * 64) {
-    const int b = f / wpb, i = f - b * wpb;
-    float v0, v1;
-    if (halves) {
-      v0 = c.res[(4 * i) * MAXB + b] + c.res[(4 * i + 1) * MAXB + b];
-      v1 = c.res[(4 * i + 2) * MAXB + b] + c.res[(4 * i + 3) * MAXB + b];
-    } else {
-      v0 = c.res[(2 * i) * MAXB + b];
-      v1 = c.res[(2 * i + 1) * MAXB + b];
-    }
-    const uint32_t lo = f2bf(v0), hi = f2bf(v1);
-    const size_t word = base + (size_t)b * stride + a0 / 2 + i;
-    if (w.op != MKD_OP_QKV) st_all(c.ws, word, tw_make(lo | (hi << 16), tag));
-    else if (local) st_local(c.ws.tw(word), tw_make(lo | (hi << 16), tag));
-    else st_co(c.ws.tw(word), tw_make(lo | (hi << 16), tag));
+  switch (w.op) {
+    case MKD_OP_QKV: p4_store_op<B, MKD_OP_QKV>(c, w); break;
+    case MKD_OP_OPROJ: p4_store_op<B, MKD_OP_OPROJ>(c, w); break;
+    case MKD_OP_GATEUP: p4_store_op<B, MKD_OP_GATEUP>(c, w); break;
+    case MKD_OP_DOWN: p4_store_op<B, MKD_OP_DOWN>(c, w); break;
+    default: break;
   }
 }
 
@@ -703,7 +820,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   uint32_t wnw = 0;
   float c0 = 0.f, c1 = 0.f, s0 = 0.f, s1 = 0.f;
   if (wave < 3) {
-    wnw = reinterpret_cast<const uint32_t*>(p4_wptr(d, layer, wave < 2 ? MKD_W_Q_NORM : MKD_W_K_NORM))[lane];
+    wnw = ldg(reinterpret_cast<const uint32_t*>(p4_wptr(d, layer, wave < 2 ? MKD_W_Q_NORM : MKD_W_K_NORM)) + lane);
     const int j = (2 * lane) & 63;
     const float* cs = d.rope_cos + (size_t)pos * (HD / 2);
     const float* sn = d.rope_sin + (size_t)pos * (HD / 2);
@@ -713,6 +830,9 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
 
   uint64_t qv[1];
   bool ok = poll_finish<1>(qaddr, qfirst, qv, tag, c.ws);
+#ifdef MKD_TRACE_POLL
+  if (tr != nullptr && lane == 0) atomicMax(reinterpret_cast<unsigned long long*>(tr + 1), (unsigned long long)wall_clock64());
+#endif
   const uint32_t word = (uint32_t)qv[0];  // dims 2*lane, 2*lane + 1
   uint32_t outw = word;
   if (wave < 3) {
@@ -731,7 +851,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     float o0, o1;
     if (lane < 32) { o0 = n0 * c0 - p0 * s0; o1 = n1 * c1 - p1 * s1; }
     else { o0 = n0 * c0 + p0 * s0; o1 = n1 * c1 + p1 * s1; }
-    outw = f2bf(o0) | (f2bf(o1) << 16);
+    outw = pack_bf2(o0, o1);
   }
   uint16_t* dst = wave < 2 ? qb + wave * HD : (wave == 2 ? kb : vb);
   reinterpret_cast<uint32_t*>(dst)[lane] = outw;
@@ -745,6 +865,11 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
       reinterpret_cast<uint32_t*>(cache + layer_off + slotp * KVS)[lane] = outw;
     }
   }
+  // Loads under a lane-dependent condition are consumed on every path: a load
+  // the compiler sees unconsumed on some path stays pending in its view, and it
+  // then waits for all memory operations (write-through stores included, ~2 us)
+  // before that register is next written, in whatever task comes next.
+  asm volatile("" ::"v"(blk_new), "v"(wnw), "v"(c0), "v"(c1), "v"(s0), "v"(s1));
   if (!p4_agree(c, ok)) return false;
   if (tr != nullptr && t == 0) tr[2] = wall_clock64();
 
@@ -793,6 +918,9 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
       for (int jj = 0; jj < 8; jj++) { a0[jj] += w0[e] * vf[jj]; a1[jj] += w1[e] * vf[jj]; }
     }
   }
+  // (as above, for the first sub-tile's loads; one dword of each load is enough)
+  asm volatile("" ::"v"(kreg[0].x), "v"(kreg[1].x), "v"(kreg[2].x), "v"(kreg[3].x), "v"(vreg[0].x), "v"(vreg[1].x),
+               "v"(vreg[2].x), "v"(vreg[3].x));
   if (wave == 0 && p_begin <= pos && pos < p_end) {
     const uint32_t kw = reinterpret_cast<const uint32_t*>(kb)[lane];
     const float t0s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb)[lane], 0.f)) * ATTN_SCALE;
@@ -878,8 +1006,13 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   }
   const uint32_t mine = f2bf(num / den);
   const uint32_t nbr = __shfl_xor(mine, 1, 64);
-  if ((dd & 1) == 0)
-    st_all(c.ws, TW_ATTN + (size_t)b * (QS / 2) + ((GROUP * h + g) * HD + dd) / 2, tw_make(mine | (nbr << 16), tag));
+  {
+    // the pair (dd, dd + 1) as one word; the even lane stores replicas 0-3, the odd one 4-7
+    const uint64_t v = tw_make((dd & 1) ? (nbr | (mine << 16)) : (mine | (nbr << 16)), tag);
+    const size_t word = TW_ATTN + (size_t)b * (QS / 2) + ((GROUP * h + g) * HD + dd) / 2;
+#pragma unroll
+    for (int r = 0; r < TW_NREP / 2; r++) st_rep(c.ws, word, (dd & 1) * (TW_NREP / 2) + r, v);
+  }
   return p4_agree(c, ok);  // also frees the scratch for the next task
 }
 
@@ -1111,9 +1244,9 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
     p4_dma<B>(d.layer_ptrs, d.embed, row, n_inst, ring, wave - PK_CW, dbg_dw);
     return;
   }
-  const P4 c{ws, (int)(blockIdx.x % TW_NREP), p4_xcc_id(), (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch)}, flags,
+  P4 c{ws, (int)(blockIdx.x % TW_NREP), p4_xcc_id(), (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch)}, flags,
              reinterpret_cast<float*>(scratch + P4_SCR_RED), reinterpret_cast<float*>(scratch + P4_SCR_RES), xs,
-             scratch + P4_SCR_ATTN};
+             scratch + P4_SCR_ATTN, reinterpret_cast<uint32_t*>(scratch + P4_SCR_STAGE), 0, nullptr};
   bool aborted = false;
   int cc = 0;
   cint32_t* crow = as_const(row);
@@ -1121,8 +1254,10 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
   for (int i = 0; i < n_inst; i++) {
     const Inst w = w_next;
     if (i + 1 < n_inst) w_next = load_inst(crow + (i + 1) * MKD_INST_WORDS);  // in flight during this task
-    uint64_t* tr = d.trace != nullptr ? d.trace + ((size_t)blockIdx.x * s.max_inst + i) * 4 : nullptr;
+    uint64_t* tr = d.trace != nullptr ? d.trace + ((size_t)blockIdx.x * s.max_inst + i) * P4_TR_STRIDE : nullptr;
     if (tr != nullptr && threadIdx.x == 0) tr[0] = wall_clock64();
+    c.trp = tr;
+    if (w.op == MKD_OP_QKV || w.op == MKD_OP_GATEUP) c.par ^= 1;
     if (w.op == MKD_OP_ATTN) {
       if (!aborted) aborted = !p4_attn<B>(d, c, w.layer, w.a0, w.a1, w.a2, tr);
       if (tr != nullptr && threadIdx.x == 0) tr[3] = wall_clock64();
