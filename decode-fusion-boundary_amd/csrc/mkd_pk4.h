@@ -41,6 +41,7 @@ constexpr int P4_STAGE_WORDS = 2 * MAXB * 2;
 constexpr int P4_SCR_RES = 1024;     // float [P4_MAX_ROWS][MAXB] task results
 constexpr int P4_SCR_ATTN = 2048;    // attention scratch (6 KiB)
 static_assert(P4_SCR_RES + 4 * P4_MAX_ROWS * MAXB <= P4_SCR_ATTN, "result tile overlaps");
+
 static_assert(P4_SCR_RED + 2 * 4 * PK_CW * MAXB <= P4_SCR_STAGE && P4_SCR_STAGE + 4 * 2 * P4_STAGE_WORDS <= P4_SCR_RES,
               "staging area overlaps");
 static_assert(P4_SCR_ATTN + 6144 <= PK_SCRATCH, "attention scratch too large");
@@ -60,13 +61,9 @@ __device__ __forceinline__ int p4_tid() {
 __device__ __forceinline__ int p4_xcc_id() {
   return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));
 }
-// Store for a consumer on the same XCD: a plain store lands in the XCD's shared
-// L2, where the consumer's device-coherent load finds it (a write-through store
-// would first have to reach the memory-side cache, ~5x slower measured).
-__device__ __forceinline__ void st_local(uint64_t* p, uint64_t v) {
-  asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
-}
 // Words every workgroup reads have one write-through copy per XCD replica.
+// (Words with readers on one XCD only are write-through stores as well: plain
+// stores kept in that XCD's L2 measured no faster in the decode step.)
 // One replica of a word every workgroup reads. Callers spread the replicas of
 // a word over lanes: a store instruction costs the same with 1 or 64 active
 // lanes, and a wave with more than 63 stores in flight stalls its issue until
@@ -116,8 +113,7 @@ struct SyncLds {
 // Compute-wave context (all fields in registers or LDS).
 struct P4 {
   Ws ws;
-  int rep;          // replica of the all-read buffers this workgroup polls (= its XCD slot)
-  int xcc;          // XCD this workgroup runs on (hardware register)
+  int rep;          // replica of the all-read buffers this workgroup polls: its XCD's
   uint32_t epoch;
   SyncLds sync;
   int* flags;
@@ -131,6 +127,7 @@ struct P4 {
                     // and the next task to write that buffer comes after another staging
                     // task, behind that task's barriers.
   uint64_t* trp;    // this task's trace record (debug builds with MKD_TRACE_POLL)
+  int task;         // index of the current task in this workgroup's row
 };
 
 #ifdef MKD_TRACE_POLL
@@ -208,11 +205,19 @@ __device__ __forceinline__ bool poll_tagged(Addr addr, uint64_t (&v)[N], uint32_
   return poll_finish<N>(addr, a, v, tag, ws);
 }
 
-// Compute-wave barrier that also ORs an abort flag over the four waves.
+// Compute-wave barrier that also agrees on an abort over the four waves.
+// flags[0] holds the index of the first task that failed in any wave (INT_MAX
+// while none has): a wave that already runs a later task may record its failure
+// before a slower wave reads the flag for this task, and comparing indices keeps
+// that later failure from aborting this task in the slow wave only. Every wave
+// thus aborts at the same task and all waves run the same sequence of barriers.
+__device__ __forceinline__ void p4_fail(const P4& c) {
+  __hip_atomic_fetch_min(c.flags, c.task, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 __device__ __forceinline__ bool p4_agree(const P4& c, bool ok) {
-  if (!ok) c.flags[0] = 1;
+  if (!ok) p4_fail(c);
   c.sync();
-  return c.flags[0] == 0;
+  return c.flags[0] > c.task;
 }
 
 constexpr int largest_divisor_le8(int n) {
@@ -356,10 +361,29 @@ __device__ __forceinline__ float lane_value(float v, int l) {
 //   K = 2048 (4 rows):  wave w -> row w
 //   K = 3072 (2 rows):  wave w -> half (w & 1) of row w >> 1; out(2 * row + half)
 // out(i, acc) gets the wave-uniform sums acc[B]; only rows < nr are reported.
-template <int B, int K, class Out>
-__device__ __forceinline__ void chunk_gemv4(const uint8_t* slot, int nr, const uint16_t* xs, Out out) {
+// The lane's activation operands come from an X source: get(b, c) is operand c
+// (8 bf16) of row b in the layout above.
+template <int K>
+struct GemvShape {
+  static constexpr int PARTS = K == 3072 ? 2 : 1;             // waves per row (K > 1024)
+  static constexpr int CPL = K == 1024 ? 4 : K / PARTS / 512;  // operands (uint4) per lane
+};
+// X source: the activations in LDS (bf16 [B][K]). (Polling them straight into
+// registers instead, each wave all of its operands, measured slower: four
+// times the polling loads outweigh the staging copy and its barrier.)
+template <int K>
+struct XLds {
+  const uint4* x4;
+  __device__ __forceinline__ uint4 get(int b, int c) const {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if constexpr (K == 1024) return x4[b * (K / 8) + c * 32 + (lane & 31)];
+    constexpr int CPL = GemvShape<K>::CPL;
+    return x4[b * (K / 8) + (wave % GemvShape<K>::PARTS) * (CPL * 64) + c * 64 + lane];
+  }
+};
+template <int B, int K, class X, class Out>
+__device__ __forceinline__ void chunk_gemv4(const uint8_t* slot, int nr, const X& xsrc, Out out) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const uint4* x4 = reinterpret_cast<const uint4*>(xs);
   if constexpr (K == 1024) {
     const int half = lane >> 5, l = lane & 31;
     const uint4* w4 = reinterpret_cast<const uint4*>(slot + (size_t)(2 * wave + half) * (K * 2));
@@ -371,7 +395,7 @@ __device__ __forceinline__ void chunk_gemv4(const uint8_t* slot, int nr, const u
     for (int b = 0; b < B; b++) {
       uint4 xv[4];  // all of this row's operand loads before its dot products
 #pragma unroll
-      for (int c = 0; c < 4; c++) xv[c] = x4[b * (K / 8) + c * 32 + l];
+      for (int c = 0; c < 4; c++) xv[c] = xsrc.get(b, c);
       acc[b] = 0.f;
 #pragma unroll
       for (int c = 0; c < 4; c++) acc[b] = dot8(wv[c], xv[c], acc[b]);
@@ -396,7 +420,7 @@ __device__ __forceinline__ void chunk_gemv4(const uint8_t* slot, int nr, const u
     for (int b = 0; b < B; b++) {
       uint4 xv[CPL];
 #pragma unroll
-      for (int c = 0; c < CPL; c++) xv[c] = x4[b * (K / 8) + part * (CPL * 64) + c * 64 + lane];
+      for (int c = 0; c < CPL; c++) xv[c] = xsrc.get(b, c);
       acc[b] = 0.f;
 #pragma unroll
       for (int c = 0; c < CPL; c++) acc[b] = dot8(wv[c], xv[c], acc[b]);
@@ -473,9 +497,9 @@ struct P4G {
 
 // The chunk loop of one GEMV task (the op is fixed for the whole loop).
 // out(i, j, acc): result i of chunk j (see chunk_gemv4 for i).
-template <int B, int K, int NS, class Out>
+template <int B, int K, int NS, class X, class Out>
 __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int rows, bool aborted, uint64_t* tr,
-                                          const uint16_t* xs, Out out, uint64_t* dbg_chunks = nullptr) {
+                                          const X& xsrc, Out out, uint64_t* dbg_chunks = nullptr) {
   (void)dbg_chunks;
   constexpr int RPC = K == 1024 ? 8 : (K == 2048 ? 4 : 2);
   uint8_t* slot = ring + (cc % NS) * SLOT_BYTES;
@@ -490,7 +514,7 @@ __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int ro
     uint64_t* ct = dbg_chunks == nullptr ? nullptr : dbg_chunks + ((size_t)blockIdx.x * 512 + ((cc + j) & 511)) * 2;
     if (ct != nullptr && threadIdx.x == 0) ct[0] = wall_clock64();
 #endif
-    if (!aborted) chunk_gemv4<B, K>(slot, min(RPC, rows - j * RPC), xs, [&](int i, const float* acc) { out(i, j, acc); });
+    if (!aborted) chunk_gemv4<B, K>(slot, min(RPC, rows - j * RPC), xsrc, [&](int i, const float* acc) { out(i, j, acc); });
 #ifdef MKD_TRACE_CHUNKS
     if (ct != nullptr && threadIdx.x == 0) ct[1] = wall_clock64();
 #endif
@@ -524,16 +548,17 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
       if (lane < B) res[(j * rpc * per_row + i) * MAXB + lane] = pick_lane<B>(acc, lane);
     };
   };
+  const uint4* x4 = reinterpret_cast<const uint4*>(c.xs);
   switch (w.op) {
     case MKD_OP_QKV:
-    case MKD_OP_GATEUP: p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(8, 1), dbg); break;
-    case MKD_OP_OPROJ: p4_chunks<B, QS, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(4, 1), dbg); break;
+    case MKD_OP_GATEUP: p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, to_res(8, 1), dbg); break;
+    case MKD_OP_OPROJ: p4_chunks<B, QS, NS>(ring, cc, nch, rows, aborted, tr, XLds<QS>{x4}, to_res(4, 1), dbg); break;
     // DOWN: two half-row partials per row, result tile entries 2 * row + half
-    case MKD_OP_DOWN: p4_chunks<B, I, NS>(ring, cc, nch, rows, aborted, tr, c.xs, to_res(2, 2), dbg); break;
+    case MKD_OP_DOWN: p4_chunks<B, I, NS>(ring, cc, nch, rows, aborted, tr, XLds<I>{x4}, to_res(2, 2), dbg); break;
     case MKD_OP_LMHEAD: {
       uint16_t* logits = d.out_logits;
       const int a0 = w.a0;
-      p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, c.xs, [&](int r, int j, const float* acc) {
+      p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, [&](int r, int j, const float* acc) {
         const int row = a0 + j * 8 + r;
 #pragma unroll
         for (int b = 0; b < B; b++) {
@@ -593,13 +618,6 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
   const int fo = (t & 63) * PK_CW + (t >> 6);
   const int n = (w.a1 >> 1) << (LB + LR);  // (channel or row) pairs x rows x replicas
   uint8_t* const twb = reinterpret_cast<uint8_t*>(c.ws.tw(BASE + (uint32_t)(w.a0 >> 1)));
-  bool local = false;
-  if (OP == MKD_OP_QKV) {
-    // read only by the attention tasks of the KV head, placed on XCD (head % 8)
-    const int a0 = w.a0;
-    const int head = a0 < QS ? a0 / (GROUP * HD) : (a0 < QS + KVS ? (a0 - QS) / HD : (a0 - QS - KVS) / HD);
-    local = c.xcc == head % TW_NREP;
-  }
   for (int e = fo; e < n; e += PK_CW * 64) {
     const int r = e & ((1 << LR) - 1), b = (e >> LR) & (B - 1), i = e >> (LR + LB);
     float v0, v1;
@@ -622,8 +640,7 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
     const uint64_t v = tw_make(pack_bf2(v0, v1), tag);
     const uint32_t off = ((uint32_t)r * (uint32_t)TW_GROUP + (uint32_t)b * STRIDE + (uint32_t)i) * 8u;
     uint64_t* q = reinterpret_cast<uint64_t*>(twb + off);
-    if (OP == MKD_OP_QKV && local) st_local(q, v);
-    else st_co(q, v);
+    st_co(q, v);
   }
   if (OP == MKD_OP_QKV) p4_publish_residual<B, QKV_N / 256>(c, w, TW_RES1, tag);
   if (OP == MKD_OP_GATEUP) p4_publish_residual<B, I / 256>(c, w, TW_RES2, tag);
@@ -853,6 +870,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     else { o0 = n0 * c0 + p0 * s0; o1 = n1 * c1 + p1 * s1; }
     outw = pack_bf2(o0, o1);
   }
+  p4_trace_at(c, 4);
   uint16_t* dst = wave < 2 ? qb + wave * HD : (wave == 2 ? kb : vb);
   reinterpret_cast<uint32_t*>(dst)[lane] = outw;
   // the new token's K (wave 2) and V (wave 3) go to their cache slot from registers
@@ -973,14 +991,12 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   if (nsplit > 1) {
     const size_t pbase = TW_APART + (((size_t)b * NKV + h) * MAXS) * PART_STRIDE;
     if (split != nsplit - 1) {
-      // read only by the last split of this (row, head), placed on the same XCD
+      // read only by the last split of this (row, head)
       uint64_t* part = c.ws.tw(pbase + (size_t)split * PART_STRIDE);
-      const bool local = c.xcc == h % TW_NREP;
-      auto put = [&](uint64_t* q, uint64_t v) { if (local) st_local(q, v); else st_co(q, v); };
-      put(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
+      st_co(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
       if (dd == 0) {
-        put(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
-        put(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
+        st_co(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
+        st_co(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
       }
       c.sync();  // the scratch is reused by this workgroup's next task
       return true;
@@ -1212,7 +1228,11 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
     const int e = min(g * G + G, issued);   // end of group g (issued >= e: 2G <= NS)
     wait_chunk<Cfg::NS - 1>(issued - e);     // chunk e - 1 (and all before) landed
     raw_barrier();
+#ifdef MKD_EXP_LOOKAHEAD
+    while (cur.nch > 0 && issued < g * G + min(Cfg::NS, MKD_EXP_LOOKAHEAD)) issue_one();
+#else
     while (cur.nch > 0 && issued < g * G + Cfg::NS) issue_one();
+#endif
   }
 }
 
@@ -1230,7 +1250,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
   int* flags = reinterpret_cast<int*>(scratch + P4_SCR_FLAGS);
   if (threadIdx.x == 0) {
     *reinterpret_cast<uint32_t*>(scratch) = 0u;  // SyncCW counter
-    flags[0] = 0;
+    flags[0] = 0x7fffffff;  // no task failed
     flags[1] = (int)ld_co(ws.line(CTR_EPOCH));
   }
   __syncthreads();
@@ -1244,9 +1264,9 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
     p4_dma<B>(d.layer_ptrs, d.embed, row, n_inst, ring, wave - PK_CW, dbg_dw);
     return;
   }
-  P4 c{ws, (int)(blockIdx.x % TW_NREP), p4_xcc_id(), (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch)}, flags,
+  P4 c{ws, p4_xcc_id() % TW_NREP, (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch)}, flags,
              reinterpret_cast<float*>(scratch + P4_SCR_RED), reinterpret_cast<float*>(scratch + P4_SCR_RES), xs,
-             scratch + P4_SCR_ATTN, reinterpret_cast<uint32_t*>(scratch + P4_SCR_STAGE), 0, nullptr};
+             scratch + P4_SCR_ATTN, reinterpret_cast<uint32_t*>(scratch + P4_SCR_STAGE), 0, nullptr, 0};
   bool aborted = false;
   int cc = 0;
   cint32_t* crow = as_const(row);
@@ -1257,6 +1277,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
     uint64_t* tr = d.trace != nullptr ? d.trace + ((size_t)blockIdx.x * s.max_inst + i) * P4_TR_STRIDE : nullptr;
     if (tr != nullptr && threadIdx.x == 0) tr[0] = wall_clock64();
     c.trp = tr;
+    c.task = i;
     if (w.op == MKD_OP_QKV || w.op == MKD_OP_GATEUP) c.par ^= 1;
     if (w.op == MKD_OP_ATTN) {
       if (!aborted) aborted = !p4_attn<B>(d, c, w.layer, w.a0, w.a1, w.a2, tr);
