@@ -155,6 +155,9 @@ int launch_persistent_b(const MkdStepDesc& d, const MkdSchedule& s, hipStream_t 
   if (d.flags & MKD_FLAG_PK_V1) {
     hipLaunchKernelGGL(k_persistent<B>, dim3(s.grid), dim3(NT), 0, st, d, s);
   } else if (d.flags & MKD_FLAG_PK_TAGGED) {
+    // its DMA waves stage 32-position KV chunks that must not straddle a cache block
+    if (d.block_size % KV_CHUNK != 0)
+      return fail(MKD_E_INVALID, "the tagged persistent kernel needs a block_size that is a multiple of 32");
     static bool attr_set4 = false;  // per instantiation; set before the first launch
     if (!attr_set4) {
       MKD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_persistent4<B>),

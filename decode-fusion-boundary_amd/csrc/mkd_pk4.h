@@ -731,75 +731,101 @@ __device__ __forceinline__ float xor16_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Cache row of position p in the row's block table (block clamped into the cache).
-__device__ __forceinline__ size_t attn_slot(cint32_t* table, int bs, int nblk, int p) {
-  return (size_t)min(max(table[p / bs], 0), nblk - 1) * bs + p % bs;
+// Positions of one ATTN task: split `split` of `nsplit` covers [p_begin, p_end)
+// of the row's pos + 1 positions (splits of a multiple of 64 positions); the
+// cached ones, [p_begin, c_end), come in KV chunks of 32 positions that the DMA
+// waves stage in the LDS ring; the token's own position (pos) is not in the
+// cache yet and comes from this step's k and v. Computed identically by the
+// DMA waves (chunk count) and the compute waves.
+constexpr int KV_CHUNK = 32;  // positions per KV chunk: 32 K rows (8 KiB) + 32 V rows (8 KiB)
+struct AttnGeo {
+  int pos, p_begin, p_end, c_end, nch;
+  bool live;  // a row of this step with a valid position
+};
+__device__ __forceinline__ AttnGeo attn_geo(int rows, int b, int pos_in, int page_stride, int bs, int split,
+                                            int nsplit) {
+  AttnGeo g;
+  g.live = b < rows && pos_in >= 0 && pos_in < MKD_MAX_POSITION && pos_in / bs < page_stride;
+  g.pos = g.live ? pos_in : 0;
+  const int ctx = g.pos + 1;
+  const int chunk = ((ctx + nsplit - 1) / nsplit + 63) & ~63;
+  g.p_begin = split * chunk;
+  g.p_end = min(ctx, g.p_begin + chunk);
+  g.c_end = min(g.p_end, g.pos);
+  g.nch = g.c_end > g.p_begin ? (g.c_end - g.p_begin + KV_CHUNK - 1) / KV_CHUNK : 0;
+  return g;
 }
-// Cached K/V of the sub-tile t0 .. t0 + 15 (positions >= c_end repeat t0):
-// K in the scores layout (lane: position pl, dims 32 quarter ..), V in the P*V
-// layout (lane: positions 4 pg + i, dims dg ..). With bs a multiple of 16 the
-// sub-tile lies in one block: one wave-uniform table lookup.
-__device__ __forceinline__ void attn_load_subtile(uint4 (&kreg)[4], uint4 (&vreg)[4], const uint16_t* kbase,
-                                                  const uint16_t* vbase, cint32_t* table, int bs, int nblk, int t0,
-                                                  int c_end, int pl, int quarter, int pg, int dg) {
-  const int pk = t0 + pl < c_end ? t0 + pl : t0;
-  size_t rowk, rowv[4];
-  if (bs % 16 == 0) {
-    const size_t base = (size_t)min(max(table[t0 / bs], 0), nblk - 1) * bs - (size_t)(t0 / bs) * bs;
-    rowk = base + pk;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int pv = t0 + 4 * pg + i < c_end ? t0 + 4 * pg + i : t0;
-      rowv[i] = base + pv;
-    }
-  } else {
-    rowk = attn_slot(table, bs, nblk, pk);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int pv = t0 + 4 * pg + i < c_end ? t0 + 4 * pg + i : t0;
-      rowv[i] = attn_slot(table, bs, nblk, pv);
-    }
-  }
-  const uint4* krow = reinterpret_cast<const uint4*>(kbase + rowk * KVS + quarter * 32);
-#pragma unroll
-  for (int i = 0; i < 4; i++) kreg[i] = krow[i];
-#pragma unroll
-  for (int i = 0; i < 4; i++) vreg[i] = *reinterpret_cast<const uint4*>(vbase + rowv[i] * KVS + dg);
+// LDS layout of a KV chunk: K row of chunk position p (0..31) at p * 256 bytes,
+// its 16-byte piece q at slot ((q + (p & 1)) & 15) (consecutive positions
+// shifted by one piece, so the scores' reads, 8 positions x 8 pieces per
+// instruction, spread over all banks); V row p at 8192 + p * 256, unswizzled.
+__device__ __forceinline__ int kv_kpiece(int p, int q) { return p * 256 + ((q + (p & 1)) & 15) * 16; }
+constexpr int KV_V_OFF = KV_CHUNK * 256;
+
+// Sums and maxima over the lanes of a wave that hold one value per group of 8
+// lanes (lanes 8p .. 8p + 7 replicate value p): xor 8 within a row of 16 lanes
+// (row_ror:8), then xor 16 and xor 32 (permlane swaps).
+__device__ __forceinline__ float sum_over_8_groups(float x) {
+  x += dpp_mov<0x128>(x, 0.f);
+  return xor32_sum(xor16_sum(x));
+}
+__device__ __forceinline__ float max_over_8_groups(float x) {
+  x = fmaxf(x, dpp_mov<0x128>(x, -INFINITY));
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Sum over the 8 lanes 8p .. 8p + 7 (quad swaps, then the other quad by half-row mirror).
+__device__ __forceinline__ float sum_within_8(float x) {
+  x += dpp_mov<0xB1>(x, 0.f);
+  x += dpp_mov<0x4E>(x, 0.f);
+  return x + dpp_mov<0x141>(x, 0.f);
+}
+
+// The hand-over barriers of a task's nch chunks without using them (a task
+// skipped after an abort: the DMA waves issue and hand over its chunks anyway).
+template <int NS>
+__device__ __forceinline__ void p4_skip_chunks(int cc, int nch) {
+  for (int j = 0; j < nch; j++)
+    if ((cc + j) % P4G<NS>::G == 0) raw_barrier();
+}
+// KV chunk count of an ATTN task (as the DMA waves compute it).
+__device__ __forceinline__ int p4_attn_chunks(const MkdStepDesc& d, const Inst& w) {
+  const int b = w.a0 / NKV;
+  const int pos_in = b < d.rows ? as_const(d.cache_seqlens)[b] : 0;
+  return attn_geo(d.rows, b, pos_in, d.page_stride, d.block_size, w.a1, w.a2).nch;
 }
 
 // ATTN task (row b, KV head h, split of nsplit of the row's positions).
-// Everything that does not depend on this step's q/k/v is requested before
-// its words are polled: the row's position and pages, the q/k norm weights,
-// the RoPE row and the first cached K/V of each wave. After the poll: q/k
-// RMSNorm + RoPE in registers, the new token's K/V written to its cache slot
-// (split 0 of an active row) straight from registers, then online softmax over
-// the split's cached positions in sub-tiles of 16 positions, one per wave and
-// round (positions p_begin + 16 w + 64 r):
-//   scores: lane (position p = lane & 15, dim quarter lane >> 4) dots 32 dims
-//           of K with both q heads; the quarters are summed with permlane swaps;
-//   P * V:  lane (8 dims (lane & 15) * 8, 4 positions 4 (lane >> 4) + i), with
-//           the 16 probabilities passed through LDS.
-// The four position groups and the four waves are merged at the end; the
-// token's own K/V (not yet in the cache when this task reads it) comes from
-// registers. The last split folds in the other splits' tagged partials.
-template <int B>
+// The task's cached K/V arrive as KV chunks in the LDS ring (staged by the DMA
+// waves like weight rows), so the compute waves issue no cache loads of their
+// own: their only global loads before the q/k/v poll are the norm weights and
+// the RoPE row, issued first, and the poll's rounds queue behind nothing else.
+// After the poll: q/k RMSNorm + RoPE in registers, the new token's K/V written
+// to its cache slot (split 0 of an active row) straight from registers, then
+// online softmax over the chunks, each chunk's 32 positions split over the four
+// waves (wave w: positions 8w .. 8w + 7):
+//   scores: lane (position p = lane >> 3, dims 16 (lane & 7) ..) dots 16 dims of
+//           K with both q heads, summed over the 8 lanes of the position;
+//   P * V:  lane (dims 2 lane, 2 lane + 1) over the wave's 8 positions, with the
+//           probabilities read from the lanes that hold them.
+// The four waves are merged at the end; the token's own K/V (not yet in the
+// cache when this task reads it) comes from LDS. The last split folds in the
+// other splits' tagged partials. nch returns the task's KV chunk count.
+template <int B, int NS>
 __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int bh, int split, int nsplit,
-                                        uint64_t* tr) {
-#ifdef MKD_PROBE_NO_ATTN
-  return true;
-#endif
+                                        uint64_t* tr, uint8_t* ring, int cc, int& nch) {
   const int t = p4_tid(), wave = t >> 6, lane = t & 63;
   const uint32_t tag = p4_tag(c.epoch, layer);
   const int b = bh / NKV, h = bh % NKV;
-  bool live = b < d.rows;
-  int pos = live ? as_const(d.cache_seqlens)[b] : 0;
   const int bs = d.block_size;
-  if (live && (pos < 0 || pos >= MKD_MAX_POSITION || pos / bs >= d.page_stride)) {
-    if (t == 0) st_co(c.ws.line(CTR_ERR), ERR_BAD_INPUT);
-    live = false;
-    pos = 0;
-  }
-  const bool active = live && as_const(d.row_active)[b] != 0;
+  const int pos_in = b < d.rows ? as_const(d.cache_seqlens)[b] : 0;
+  const AttnGeo ag = attn_geo(d.rows, b, pos_in, d.page_stride, bs, split, nsplit);
+  nch = ag.nch;
+  if (b < d.rows && !ag.live && t == 0) st_co(c.ws.line(CTR_ERR), ERR_BAD_INPUT);
+  const int pos = ag.pos, p_begin = ag.p_begin, p_end = ag.p_end, c_end = ag.c_end;
+  const bool active = ag.live && as_const(d.row_active)[b] != 0;
   cint32_t* table = as_const(d.page_table + (size_t)b * d.page_stride);
   const int nblk = d.num_blocks;
   uint8_t* smem = c.attn_smem;
@@ -808,32 +834,10 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   uint16_t* vb = kb + HD;                                 // [128] v
   float* mrg = reinterpret_cast<float*>(smem + 1024);     // [4 waves][2][128]
   float* mrg_ml = mrg + PK_CW * GROUP * HD;               // [4][2] m, [4][2] l
-  float* pb = reinterpret_cast<float*>(c.xs) + wave * 32; // [2][16] this wave's probabilities (xs is free here)
-
-  const int ctx = pos + 1;
-  const int chunk = ((ctx + nsplit - 1) / nsplit + 63) & ~63;
-  const int p_begin = split * chunk;
-  const int p_end = min(ctx, p_begin + chunk);
-  const int c_end = min(p_end, pos);  // cached positions of this split
-  const int pl = lane & 15, quarter = lane >> 4;   // scores: position, dim quarter
-  const int dg = (lane & 15) * 8, pg = lane >> 4;  // P*V: dims, position group
   const size_t layer_off = (size_t)layer * (size_t)d.kv_layer_stride + (size_t)h * HD;
-  const uint16_t* kbase = d.k_cache + layer_off;
-  const uint16_t* vbase = d.v_cache + layer_off;
-  uint4 kreg[4], vreg[4];
-  // this step's q (waves 0, 1: heads 2h, 2h+1), k (wave 2), v (wave 3): one word per
-  // lane; its first poll load goes out before every other load of the task
-  size_t src;
-  if (wave < 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + (size_t)(GROUP * h + wave) * (HD / 2) + lane;
-  else if (wave == 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + QS / 2 + (size_t)h * (HD / 2) + lane;
-  else src = TW_QKV + (size_t)b * (QKV_N / 2) + (QS + KVS) / 2 + (size_t)h * (HD / 2) + lane;
-  auto qaddr = [=](int) { return c.ws.tw(src); };
-  uint64_t qfirst[1];
-  poll_issue<1>(qaddr, qfirst);
-  const int first_t0 = p_begin + wave * 16;
-  if (first_t0 < c_end)
-    attn_load_subtile(kreg, vreg, kbase, vbase, table, bs, nblk, first_t0, c_end, pl, quarter, pg, dg);
-  // static operands of the norm/RoPE step, and the new token's cache slot
+
+  // static operands of the norm/RoPE step and the new token's cache slot: loaded
+  // before the poll (the poll's first check then also covers them)
   uint32_t wnw = 0;
   float c0 = 0.f, c1 = 0.f, s0 = 0.f, s1 = 0.f;
   if (wave < 3) {
@@ -844,9 +848,13 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     c0 = cs[j]; c1 = cs[j + 1]; s0 = sn[j]; s1 = sn[j + 1];
   }
   const int blk_new = (split == 0 && active) ? table[pos / bs] : 0;
-
+  // this step's q (waves 0, 1: heads 2h, 2h+1), k (wave 2), v (wave 3): one word per lane
+  size_t src;
+  if (wave < 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + (size_t)(GROUP * h + wave) * (HD / 2) + lane;
+  else if (wave == 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + QS / 2 + (size_t)h * (HD / 2) + lane;
+  else src = TW_QKV + (size_t)b * (QKV_N / 2) + (QS + KVS) / 2 + (size_t)h * (HD / 2) + lane;
   uint64_t qv[1];
-  bool ok = poll_finish<1>(qaddr, qfirst, qv, tag, c.ws);
+  bool ok = poll_tagged<1>([=](int) { return c.ws.tw(src); }, qv, tag, c.ws);
 #ifdef MKD_TRACE_POLL
   if (tr != nullptr && lane == 0) atomicMax(reinterpret_cast<unsigned long long*>(tr + 1), (unsigned long long)wall_clock64());
 #endif
@@ -885,60 +893,55 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   }
   // Loads under a lane-dependent condition are consumed on every path: a load
   // the compiler sees unconsumed on some path stays pending in its view, and it
-  // then waits for all memory operations (write-through stores included, ~2 us)
-  // before that register is next written, in whatever task comes next.
+  // then waits for all memory operations (write-through stores included) before
+  // that register is next written, in whatever task comes next.
   asm volatile("" ::"v"(blk_new), "v"(wnw), "v"(c0), "v"(c1), "v"(s0), "v"(s1));
-  if (!p4_agree(c, ok)) return false;
+  if (!p4_agree(c, ok)) {
+    p4_skip_chunks<NS>(cc, nch);  // the DMA waves still hand the chunks over
+    return false;
+  }
   if (tr != nullptr && t == 0) tr[2] = wall_clock64();
 
-  // this lane's 32 dims of both q heads (scores layout), kept for all sub-tiles
-  uint4 qa[4], qc[4];
+  // scores layout: this lane's 16 dims of both q heads
+  const int pl = lane >> 3, part = lane & 7;
+  uint4 qa[2], qc[2];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    qa[i] = reinterpret_cast<const uint4*>(qb + quarter * 32)[i];
-    qc[i] = reinterpret_cast<const uint4*>(qb + HD + quarter * 32)[i];
+  for (int i = 0; i < 2; i++) {
+    qa[i] = reinterpret_cast<const uint4*>(qb + part * 16)[i];
+    qc[i] = reinterpret_cast<const uint4*>(qb + HD + part * 16)[i];
   }
   float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
-  float a0[8], a1[8];
-#pragma unroll
-  for (int jj = 0; jj < 8; jj++) { a0[jj] = 0.f; a1[jj] = 0.f; }
-  for (int t0 = first_t0; t0 < c_end; t0 += PK_CW * 16) {
-    if (t0 != first_t0) attn_load_subtile(kreg, vreg, kbase, vbase, table, bs, nblk, t0, c_end, pl, quarter, pg, dg);
-    float sc0 = 0.f, sc1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      sc0 = dot8(kreg[i], qa[i], sc0);
-      sc1 = dot8(kreg[i], qc[i], sc1);
-    }
-    sc0 = xor32_sum(xor16_sum(sc0));  // full 128-dim scores, replicated over the quarters
-    sc1 = xor32_sum(xor16_sum(sc1));
-    const bool valid = t0 + pl < c_end;
+  float a00 = 0.f, a01 = 0.f, a10 = 0.f, a11 = 0.f;  // head g, dim 2 lane + i
+  const uint8_t* slot = ring + (cc % NS) * SLOT_BYTES;
+  const uint8_t* const ring_end = ring + NS * SLOT_BYTES;
+  const int pp = 8 * wave + pl;  // this lane's position within a chunk
+  for (int j = 0; j < nch; j++) {
+    if ((cc + j) % P4G<NS>::G == 0) raw_barrier();  // group of G chunks handed over
+    const uint4 k0 = *reinterpret_cast<const uint4*>(slot + kv_kpiece(pp, 2 * part));
+    const uint4 k1 = *reinterpret_cast<const uint4*>(slot + kv_kpiece(pp, 2 * part + 1));
+    float sc0 = sum_within_8(dot8(k1, qa[1], dot8(k0, qa[0], 0.f)));
+    float sc1 = sum_within_8(dot8(k1, qc[1], dot8(k0, qc[0], 0.f)));
+    const bool valid = p_begin + KV_CHUNK * j + pp < c_end;
     sc0 = valid ? sc0 * ATTN_SCALE : -INFINITY;
     sc1 = valid ? sc1 * ATTN_SCALE : -INFINITY;
-    const float n0 = fmaxf(m0, wave_max(sc0)), n1 = fmaxf(m1, wave_max(sc1));
-    const float al0 = expf(m0 - n0), al1 = expf(m1 - n1);
-    const float e0 = expf(sc0 - n0), e1 = expf(sc1 - n1);
-    // each position's probability is replicated 4 times over the wave
-    l0 = l0 * al0 + 0.25f * wave_sum(e0);
-    l1 = l1 * al1 + 0.25f * wave_sum(e1);
+    const float n0 = fmaxf(m0, max_over_8_groups(sc0)), n1 = fmaxf(m1, max_over_8_groups(sc1));
+    // (a wave whose positions are all past c_end keeps m = -inf, l = 0)
+    const float al0 = n0 == -INFINITY ? 1.f : expf(m0 - n0), al1 = n1 == -INFINITY ? 1.f : expf(m1 - n1);
+    const float e0 = valid ? expf(sc0 - n0) : 0.f, e1 = valid ? expf(sc1 - n1) : 0.f;
+    l0 = l0 * al0 + sum_over_8_groups(e0);
+    l1 = l1 * al1 + sum_over_8_groups(e1);
     m0 = n0; m1 = n1;
-    if (lane < 16) { pb[lane] = e0; pb[16 + lane] = e1; }
-    const float4 x = reinterpret_cast<const float4*>(pb)[pg];
-    const float4 y = reinterpret_cast<const float4*>(pb + 16)[pg];
-    const float w0[4] = {x.x, x.y, x.z, x.w}, w1[4] = {y.x, y.y, y.z, y.w};
+    a00 *= al0; a01 *= al0; a10 *= al1; a11 *= al1;
 #pragma unroll
-    for (int jj = 0; jj < 8; jj++) { a0[jj] *= al0; a1[jj] *= al1; }
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const uint4 v = vreg[e];
-      const float vf[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
-#pragma unroll
-      for (int jj = 0; jj < 8; jj++) { a0[jj] += w0[e] * vf[jj]; a1[jj] += w1[e] * vf[jj]; }
+    for (int q = 0; q < 8; q++) {
+      const float w0 = lane_value(e0, 8 * q), w1 = lane_value(e1, 8 * q);
+      const uint32_t vw = *reinterpret_cast<const uint32_t*>(slot + KV_V_OFF + (8 * wave + q) * 256 + 4 * lane);
+      a00 += w0 * bf_lo(vw); a01 += w0 * bf_hi(vw);
+      a10 += w1 * bf_lo(vw); a11 += w1 * bf_hi(vw);
     }
+    slot += SLOT_BYTES;
+    if (slot == ring_end) slot = ring;
   }
-  // (as above, for the first sub-tile's loads; one dword of each load is enough)
-  asm volatile("" ::"v"(kreg[0].x), "v"(kreg[1].x), "v"(kreg[2].x), "v"(kreg[3].x), "v"(vreg[0].x), "v"(vreg[1].x),
-               "v"(vreg[2].x), "v"(vreg[3].x));
   if (wave == 0 && p_begin <= pos && pos < p_end) {
     const uint32_t kw = reinterpret_cast<const uint32_t*>(kb)[lane];
     const float t0s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb)[lane], 0.f)) * ATTN_SCALE;
@@ -949,26 +952,13 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     l0 = l0 * al0 + e0;
     l1 = l1 * al1 + e1;
     m0 = n0; m1 = n1;
-    const uint4 v = *reinterpret_cast<const uint4*>(vb + dg);
-    const float vf[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y), bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
-#pragma unroll
-    for (int jj = 0; jj < 8; jj++) {
-      a0[jj] = a0[jj] * al0 + (pg == 0 ? e0 * vf[jj] : 0.f);
-      a1[jj] = a1[jj] * al1 + (pg == 0 ? e1 * vf[jj] : 0.f);
-    }
+    const uint32_t vw = reinterpret_cast<const uint32_t*>(vb)[lane];
+    a00 = a00 * al0 + e0 * bf_lo(vw); a01 = a01 * al0 + e0 * bf_hi(vw);
+    a10 = a10 * al1 + e1 * bf_lo(vw); a11 = a11 * al1 + e1 * bf_hi(vw);
   }
-  // sum the four position groups (rows of 16 lanes), then merge the waves in LDS
-#pragma unroll
-  for (int jj = 0; jj < 8; jj++) {
-    a0[jj] = xor32_sum(xor16_sum(a0[jj]));
-    a1[jj] = xor32_sum(xor16_sum(a1[jj]));
-  }
-  if (lane < 16) {
-    float4* m0p = reinterpret_cast<float4*>(mrg + (wave * GROUP + 0) * HD + lane * 8);
-    float4* m1p = reinterpret_cast<float4*>(mrg + (wave * GROUP + 1) * HD + lane * 8);
-    m0p[0] = make_float4(a0[0], a0[1], a0[2], a0[3]); m0p[1] = make_float4(a0[4], a0[5], a0[6], a0[7]);
-    m1p[0] = make_float4(a1[0], a1[1], a1[2], a1[3]); m1p[1] = make_float4(a1[4], a1[5], a1[6], a1[7]);
-  }
+  // merge the waves in LDS
+  reinterpret_cast<float2*>(mrg + (wave * GROUP + 0) * HD)[lane] = make_float2(a00, a01);
+  reinterpret_cast<float2*>(mrg + (wave * GROUP + 1) * HD)[lane] = make_float2(a10, a11);
   if (lane == 0) {
     mrg_ml[wave * GROUP + 0] = m0; mrg_ml[wave * GROUP + 1] = m1;
     mrg_ml[PK_CW * GROUP + wave * GROUP + 0] = l0; mrg_ml[PK_CW * GROUP + wave * GROUP + 1] = l1;
@@ -1044,8 +1034,14 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
 //   K = 3072: units 3dw + k   -> row dw >> 1, sixth 3 (dw & 1) + k
 // A short last chunk (rows not a multiple of the chunk's) takes the general
 // path, which repeats the task's last unit to keep the copy count.
+//
+// ATTN tasks (kind 3) stage their cached K/V: chunk j = positions p0 + 32 j ..
+// + 31 (within one cache block, as the block size is a multiple of 32), K in
+// units 0-7 and V in units 8-15 (4 positions per unit), this wave's units dw,
+// dw + 4 (K) and dw + 8, dw + 12 (V), each lane one 16-byte piece; positions
+// at or past the end of the cached ones repeat p0.
 struct DmaTask {
-  int kind;              // 0: K = 1024, 1: K = 2048, 2: K = 3072
+  int kind;              // 0: K = 1024, 1: K = 2048, 2: K = 3072, 3: KV chunks of an ATTN task
   int nch;               // chunks (0: no weights)
   int nfull;             // leading full chunks
   int units;             // 1-KiB units of the task's weight rows
@@ -1056,14 +1052,71 @@ struct DmaTask {
   int64_t kstep;         // elements between this wave's units within a chunk
   int64_t cstep;         // elements between chunks
   int lds0, ldsk;        // slot offset of this wave's first unit, and between its units (bytes)
+  // ATTN tasks reuse the fields (the struct lives in scalar registers across the
+  // DMA loop; more fields would spill it to memory): b0 / b1 = K / V of the layer
+  // and head, src = the row's block table, stride = block size, units = cache
+  // blocks, nfull = first position p0, lds0 = end of the cached positions.
+  __device__ __forceinline__ cint32_t* table() const { return (cint32_t*)(uintptr_t)src; }
 };
 
-__device__ __forceinline__ DmaTask dma_decode(cuint64_t* lp, const uint16_t* emb, const Inst& w, int dw) {
+// Step-descriptor fields the DMA waves need for ATTN tasks, read from the
+// kernel arguments through the constant address space (scalar loads).
+template <typename T>
+__device__ __forceinline__ T karg_field(const uint8_t* karg, size_t off) {
+  typedef __attribute__((address_space(4))) const T ct;
+  return *reinterpret_cast<ct*>(reinterpret_cast<uintptr_t>(karg) + off);
+}
+__device__ __forceinline__ void dma_decode_attn(DmaTask& t, const uint8_t* karg, const Inst& w) {
+  const int b = w.a0 / NKV, h = w.a0 % NKV;
+  const int rows = karg_field<int32_t>(karg, offsetof(MkdStepDesc, rows));
+  const int bs = karg_field<int32_t>(karg, offsetof(MkdStepDesc, block_size));
+  const int stride = karg_field<int32_t>(karg, offsetof(MkdStepDesc, page_stride));
+  const int32_t* seqlens = karg_field<int32_t*>(karg, offsetof(MkdStepDesc, cache_seqlens));
+  const int pos_in = b < rows ? as_const(seqlens)[b] : 0;
+  const AttnGeo g = attn_geo(rows, b, pos_in, stride, bs, w.a1, w.a2);
+  t.kind = 3;
+  t.nch = g.nch;
+  if (g.nch == 0) return;
+  const size_t off = (size_t)w.layer * (size_t)karg_field<int64_t>(karg, offsetof(MkdStepDesc, kv_layer_stride)) +
+                     (size_t)h * HD;
+  t.b0 = karg_field<uint16_t*>(karg, offsetof(MkdStepDesc, k_cache)) + off;
+  t.b1 = karg_field<uint16_t*>(karg, offsetof(MkdStepDesc, v_cache)) + off;
+  t.src = reinterpret_cast<const uint16_t*>(karg_field<const int32_t*>(karg, offsetof(MkdStepDesc, page_table)) +
+                                            (size_t)b * stride);
+  t.stride = bs;
+  t.units = karg_field<int32_t>(karg, offsetof(MkdStepDesc, num_blocks));
+  t.nfull = g.p_begin;
+  t.lds0 = g.c_end;
+}
+
+// KV chunk j of ATTN task t into `slot` (this DMA wave's 4 units).
+__device__ __forceinline__ void dma_issue_attn(const DmaTask& t, int j, uint8_t* slot, int dw) {
+  const int lane = threadIdx.x & 63;
+  const int P0 = t.nfull + KV_CHUNK * j, bs = t.stride;
+  const int blk = min(max(t.table()[P0 / bs], 0), t.units - 1);
+  const size_t row0 = (size_t)blk * bs + P0 % bs;
+  const int s16 = lane & 15;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int u = dw + 4 * k;                       // k < 2: K units, k >= 2: V units
+    const int p = 4 * (u & 7) + (lane >> 4);        // chunk position of this lane
+    const int q = k < 2 ? ((s16 - (p & 1)) & 15) : s16;  // source piece (K: unswizzled)
+    const int pr = P0 + p < t.lds0 ? p : 0;
+    const uint16_t* src = (k < 2 ? t.b0 : t.b1) + (row0 + pr) * KVS + q * 8;
+    __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(slot + u * 1024), 16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ DmaTask dma_decode(cuint64_t* lp, const uint16_t* emb, const uint8_t* karg, const Inst& w,
+                                              int dw) {
   auto W = [&](int which) { return reinterpret_cast<const uint16_t*>(lp[w.layer * MKD_LAYER_PTRS + which]); };
   const int a0 = w.a0, a1 = w.a1;
   DmaTask t{};
   t.b1 = nullptr;
   switch (w.op) {
+    case MKD_OP_ATTN:
+      dma_decode_attn(t, karg, w);
+      return t;
     case MKD_OP_QKV:
       t.b0 = a0 < QS ? W(MKD_W_Q) + (size_t)a0 * H
                      : (a0 < QS + KVS ? W(MKD_W_K) + (size_t)(a0 - QS) * H : W(MKD_W_V) + (size_t)(a0 - QS - KVS) * H);
@@ -1165,7 +1218,8 @@ __device__ __forceinline__ void wait_chunk(int later) {
 // slot of chunk r - 2, which the compute waves finished before barrier r - 1.
 template <int B>
 __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* embed, const int32_t* row,
-                                    int n_inst_arg, uint8_t* ring_arg, int dw_arg, uint8_t* ws_arg) {
+                                    int n_inst_arg, uint8_t* ring_arg, int dw_arg, uint8_t* ws_arg,
+                                    const uint8_t* karg_arg) {
   using Cfg = PkCfg<B>;
   cuint64_t* lp = as_const(uniform_ptr(layer_ptrs));
   const uint16_t* emb = uniform_ptr(embed);
@@ -1173,6 +1227,7 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
   const int n = __builtin_amdgcn_readfirstlane(n_inst_arg);
   uint8_t* ring = uniform_ptr(ring_arg);
   const int dw = __builtin_amdgcn_readfirstlane(dw_arg);
+  const uint8_t* karg = uniform_ptr(karg_arg);
 #ifdef MKD_TRACE_CHUNKS
   // debug: chunk arrival/release/issue times after the compute waves' ([grid][512][3])
   uint64_t* dbg = reinterpret_cast<uint64_t*>(uniform_ptr(ws_arg));
@@ -1189,7 +1244,7 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
       const Inst w = pinst;
       pf++;
       if (pf < n) pinst = load_inst(crow + pf * MKD_INST_WORDS);
-      const DmaTask t = dma_decode(lp, emb, w, dw);
+      const DmaTask t = dma_decode(lp, emb, karg, w, dw);
       if (t.nch > 0) return t;
     }
     DmaTask none{};
@@ -1211,7 +1266,8 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
     uint8_t* slot = ring + (issued % Cfg::NS) * SLOT_BYTES;
     if (cur.kind == 0) dma_issue<H>(cur, tj, slot, dw);
     else if (cur.kind == 1) dma_issue<QS>(cur, tj, slot, dw);
-    else dma_issue<I>(cur, tj, slot, dw);
+    else if (cur.kind == 2) dma_issue<I>(cur, tj, slot, dw);
+    else dma_issue_attn(cur, tj, slot, dw);
     issued++;
     if (++tj == cur.nch) {
       tj = 0;
@@ -1261,7 +1317,8 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
 #else
     uint8_t* dbg_dw = nullptr;
 #endif
-    p4_dma<B>(d.layer_ptrs, d.embed, row, n_inst, ring, wave - PK_CW, dbg_dw);
+    p4_dma<B>(d.layer_ptrs, d.embed, row, n_inst, ring, wave - PK_CW, dbg_dw,
+              reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(__builtin_amdgcn_kernarg_segment_ptr())));
     return;
   }
   P4 c{ws, p4_xcc_id() % TW_NREP, (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch)}, flags,
@@ -1280,7 +1337,14 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
     c.task = i;
     if (w.op == MKD_OP_QKV || w.op == MKD_OP_GATEUP) c.par ^= 1;
     if (w.op == MKD_OP_ATTN) {
-      if (!aborted) aborted = !p4_attn<B>(d, c, w.layer, w.a0, w.a1, w.a2, tr);
+      int nkv = 0;
+      if (!aborted) {
+        aborted = !p4_attn<B, Cfg::NS>(d, c, w.layer, w.a0, w.a1, w.a2, tr, ring, cc, nkv);
+      } else {
+        nkv = p4_attn_chunks(d, w);
+        p4_skip_chunks<Cfg::NS>(cc, nkv);
+      }
+      cc += nkv;
       if (tr != nullptr && threadIdx.x == 0) tr[3] = wall_clock64();
       continue;
     }

@@ -19,6 +19,7 @@ INST_WORDS = 8
 MAX_LM_SLOTS = 1024
 LAYER_PTRS = 11
 TW_REPLICAS = 8          # replicas of the tagged buffers every workgroup reads (one per XCD)
+KV_CHUNK = 32            # positions per KV chunk the tagged kernel stages (block_size must be a multiple)
 
 FLAG_ADVANCE = 1
 FLAG_ZERO_FANIN = 2

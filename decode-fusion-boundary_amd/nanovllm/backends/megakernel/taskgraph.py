@@ -135,6 +135,11 @@ class TaskGraphDecoder:
         if persistent_variant not in native.PERSISTENT_VARIANTS:
             raise ValueError(f"persistent_variant must be one of {sorted(native.PERSISTENT_VARIANTS)}; "
                              f"got {persistent_variant!r}")
+        if persistent_variant == "tagged" and int(block_size) % native.KV_CHUNK != 0:
+            # the tagged kernel stages KV chunks of 32 positions that must lie in one
+            # cache block; other block sizes run the LDS-DMA kernel
+            persistent_variant = "lds_dma"
+        self.persistent_variant = persistent_variant
         self._variant_flags = native.PERSISTENT_VARIANTS[persistent_variant]
         if launch not in ("persistent", "graph"):
             raise ValueError(f"launch must be 'persistent' or 'graph'; got {launch!r}")
