@@ -248,7 +248,7 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
 // from_embed: the rows are the embedding rows of input_ids (layer 0).
 // Otherwise s = hidden + residual from two tagged [MAXB][H/2] buffers.
 // Threads res_first .. res_first + res_n - 1 stage their 4 features of bf16(s),
-// the next residual, for p4_publish_residual at the end of the task.
+// the next residual, published at the end of the task (p4_residual_word).
 template <int B>
 __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c, bool from_embed, size_t hid,
                                               size_t resid, uint32_t tag_in, const uint16_t* nw, int res_first,
@@ -578,22 +578,28 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
 
 constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
 
-// The residual words this task's owner threads staged in its prologue, one
-// store per (word, replica) spread over the waves. Issued after the task's
-// outputs: the residual is read two stages later, and stores issued before
-// the task's chunk loop would hold up the waits the compiler places there for
-// all of the wave's memory operations.
+// The residual words this task's owner threads staged in its prologue: one
+// store per (word, replica), at most one per thread (at most 2 owners x 8 rows
+// x 2 words x 8 replicas), spread over the waves. Read from LDS before the
+// task's output stores and issued after them: the residual is read two stages
+// later, and an LDS read behind the output stores made the compiler wait for
+// their write acknowledgements first.
+struct ResWord {
+  uint64_t* q;  // null: this thread has no residual store
+  uint64_t v;
+};
 template <int B, int F>
-__device__ __forceinline__ void p4_publish_residual(const P4& c, const Inst& w, size_t base, uint32_t tag) {
+__device__ __forceinline__ ResWord p4_residual_word(const P4& c, const Inst& w, size_t base, uint32_t tag) {
   const ResRange r = p4_res_range<F>(w);
   const uint32_t* stage = c.stage + c.par * P4_STAGE_WORDS;
   const int t = p4_tid();
   constexpr int LR = ilog2(TW_NREP), LB = ilog2(B);
-  for (int e = (t & 63) * PK_CW + (t >> 6); e < (r.n << (LB + 1 + LR)); e += PK_CW * 64) {
-    const int k = e >> LR, o = k >> (LB + 1), b = (k >> 1) & (B - 1);
-    const size_t word = base + (size_t)b * (H / 2) + 2 * (r.first + o) + (k & 1);
-    st_rep(c.ws, word, e & (TW_NREP - 1), tw_make(stage[k], tag));
-  }
+  static_assert(2 * B * 2 * TW_NREP <= PK_CW * 64, "one residual store per thread");
+  const int e = (t & 63) * PK_CW + (t >> 6);
+  if (e >= (r.n << (LB + 1 + LR))) return ResWord{nullptr, 0};
+  const int k = e >> LR, o = k >> (LB + 1), b = (k >> 1) & (B - 1);
+  const size_t word = base + (size_t)b * (H / 2) + 2 * (r.first + o) + (k & 1);
+  return ResWord{c.ws.tw(word + (size_t)(e & (TW_NREP - 1)) * TW_GROUP), tw_make(stage[k], tag)};
 }
 
 // Publish one GEMV task's rows as tagged bf16 pairs. Entry e = (pair i, row b,
@@ -618,6 +624,9 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
   const int fo = (t & 63) * PK_CW + (t >> 6);
   const int n = (w.a1 >> 1) << (LB + LR);  // (channel or row) pairs x rows x replicas
   uint8_t* const twb = reinterpret_cast<uint8_t*>(c.ws.tw(BASE + (uint32_t)(w.a0 >> 1)));
+  ResWord rw{nullptr, 0};
+  if (OP == MKD_OP_QKV) rw = p4_residual_word<B, QKV_N / 256>(c, w, TW_RES1, tag);
+  if (OP == MKD_OP_GATEUP) rw = p4_residual_word<B, I / 256>(c, w, TW_RES2, tag);
   for (int e = fo; e < n; e += PK_CW * 64) {
     const int r = e & ((1 << LR) - 1), b = (e >> LR) & (B - 1), i = e >> (LR + LB);
     float v0, v1;
@@ -642,8 +651,7 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
     uint64_t* q = reinterpret_cast<uint64_t*>(twb + off);
     st_co(q, v);
   }
-  if (OP == MKD_OP_QKV) p4_publish_residual<B, QKV_N / 256>(c, w, TW_RES1, tag);
-  if (OP == MKD_OP_GATEUP) p4_publish_residual<B, I / 256>(c, w, TW_RES2, tag);
+  if (rw.q != nullptr) st_co(rw.q, rw.v);
 }
 static_assert(TW_WORDS * 8 < (1ull << 32), "tagged offsets are 32-bit");
 
@@ -1264,6 +1272,10 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
   DmaTask nxt = next_weight_task();
   auto issue_one = [&]() {
     uint8_t* slot = ring + (issued % Cfg::NS) * SLOT_BYTES;
+#ifdef MKD_TRACE_CHUNKS
+    if (dbg != nullptr && dw == 0 && (threadIdx.x & 63) == 0)
+      dbg[((size_t)blockIdx.x * 512 + (issued & 511)) * 3 + 2] = wall_clock64();
+#endif
     if (cur.kind == 0) dma_issue<H>(cur, tj, slot, dw);
     else if (cur.kind == 1) dma_issue<QS>(cur, tj, slot, dw);
     else if (cur.kind == 2) dma_issue<I>(cur, tj, slot, dw);
@@ -1283,6 +1295,12 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
   for (int g = 0; g * G < issued; g++) {
     const int e = min(g * G + G, issued);   // end of group g (issued >= e: 2G <= NS)
     wait_chunk<Cfg::NS - 1>(issued - e);     // chunk e - 1 (and all before) landed
+#ifdef MKD_TRACE_CHUNKS
+    if (dbg != nullptr && dw == 0 && (threadIdx.x & 63) == 0) {
+      const uint64_t now = wall_clock64();
+      for (int k = g * G; k < e; k++) dbg[((size_t)blockIdx.x * 512 + (k & 511)) * 3] = now;
+    }
+#endif
     raw_barrier();
 #ifdef MKD_EXP_LOOKAHEAD
     while (cur.nch > 0 && issued < g * G + min(Cfg::NS, MKD_EXP_LOOKAHEAD)) issue_one();
