@@ -130,7 +130,7 @@ struct P4 {
   int task;         // index of the current task in this workgroup's row
 };
 
-#ifdef MKD_TRACE_POLL
+#if defined(MKD_TRACE_POLL) || defined(MKD_TRACE_BARRIER)
 constexpr int P4_TR_STRIDE = 8;  // debug records: slots 4.. hold points inside the prologue
 #else
 constexpr int P4_TR_STRIDE = 4;
@@ -334,9 +334,7 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
     *reinterpret_cast<uint2*>(c.xs + (size_t)b * H + k0) =
         make_uint2(pack_bf2(bf_lo(n01) * w4[0], bf_hi(n01) * w4[1]), pack_bf2(bf_lo(n23) * w4[2], bf_hi(n23) * w4[3]));
   }
-  p4_trace_at(c, 6);
   c.sync();
-  p4_trace_at(c, 7);
   return true;
 }
 
@@ -505,7 +503,15 @@ __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int ro
   uint8_t* slot = ring + (cc % NS) * SLOT_BYTES;
   uint8_t* const ring_end = ring + NS * SLOT_BYTES;
   for (int j = 0; j < nch; j++) {
+#if defined(MKD_TRACE_POLL) || defined(MKD_TRACE_BARRIER)
+    if (j == 0 && tr != nullptr && (threadIdx.x & 63) == 0)
+      atomicMax(reinterpret_cast<unsigned long long*>(tr + 6), (unsigned long long)wall_clock64());
+#endif
     if ((cc + j) % P4G<NS>::G == 0) raw_barrier();  // group of G chunks handed over
+#if defined(MKD_TRACE_POLL) || defined(MKD_TRACE_BARRIER)
+    if (j == 0 && tr != nullptr && (threadIdx.x & 63) == 0)
+      atomicMax(reinterpret_cast<unsigned long long*>(tr + 7), (unsigned long long)wall_clock64());
+#endif
 #ifndef MKD_TRACE_POLL
     if (j == 0 && tr != nullptr && threadIdx.x == 0) tr[2] = wall_clock64();
 #endif
