@@ -61,6 +61,8 @@ __device__ __forceinline__ int p4_tid() {
 __device__ __forceinline__ int p4_xcc_id() {
   return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((4 - 1) << 11));
 }
+// Store of a tagged word: device-scope, i.e. write-through to the memory-side cache.
+__device__ __forceinline__ void st_tw(uint64_t* p, uint64_t v) { st_co(p, v); }
 // Words every workgroup reads have one write-through copy per XCD replica.
 // (Words with readers on one XCD only are write-through stores as well: plain
 // stores kept in that XCD's L2 measured no faster in the decode step.)
@@ -69,7 +71,7 @@ __device__ __forceinline__ int p4_xcc_id() {
 // lanes, and a wave with more than 63 stores in flight stalls its issue until
 // write-through acknowledgements (~2 us) come back.
 __device__ __forceinline__ void st_rep(const Ws& ws, size_t word, int rep, uint64_t v) {
-  st_co(ws.tw(word + (size_t)rep * TW_GROUP), v);
+  st_tw(ws.tw(word + (size_t)rep * TW_GROUP), v);
 }
 
 // Plain load through a global-address-space pointer. A pointer read from
@@ -306,6 +308,10 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
     }
   }
   const float w4[4] = {bf_lo(wv.x), bf_hi(wv.x), bf_lo(wv.y), bf_hi(wv.y)};
+  // consumed here, before the abort return below: a load left unconsumed on
+  // that path would make the compiler wait for all memory operations at the
+  // start of every later chunk loop
+  asm volatile("" ::"v"(w4[0]), "v"(w4[1]), "v"(w4[2]), "v"(w4[3]));
   // this thread's 4 features of the new residual, when this task owns them:
   // staged in LDS as words [owner][b][2]
   if (res_owner) {
@@ -502,25 +508,30 @@ __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int ro
   constexpr int RPC = K == 1024 ? 8 : (K == 2048 ? 4 : 2);
   uint8_t* slot = ring + (cc % NS) * SLOT_BYTES;
   uint8_t* const ring_end = ring + NS * SLOT_BYTES;
+  // (no global store inside the loop: a loop with stores makes the compiler
+  // wait for all of the wave's outstanding memory operations before it, the
+  // previous task's write-through stores included)
+#ifndef MKD_TRACE_POLL
+  if (tr != nullptr && threadIdx.x == 0) tr[2] = wall_clock64();
+#endif
   for (int j = 0; j < nch; j++) {
 #if defined(MKD_TRACE_POLL) || defined(MKD_TRACE_BARRIER)
     if (j == 0 && tr != nullptr && (threadIdx.x & 63) == 0)
       atomicMax(reinterpret_cast<unsigned long long*>(tr + 6), (unsigned long long)wall_clock64());
 #endif
     if ((cc + j) % P4G<NS>::G == 0) raw_barrier();  // group of G chunks handed over
-#if defined(MKD_TRACE_POLL) || defined(MKD_TRACE_BARRIER)
-    if (j == 0 && tr != nullptr && (threadIdx.x & 63) == 0)
-      atomicMax(reinterpret_cast<unsigned long long*>(tr + 7), (unsigned long long)wall_clock64());
-#endif
-#ifndef MKD_TRACE_POLL
-    if (j == 0 && tr != nullptr && threadIdx.x == 0) tr[2] = wall_clock64();
-#endif
+
+
 #ifdef MKD_TRACE_CHUNKS
     // debug: chunk release and compute-end times after the task trace ([grid][512][2])
     uint64_t* ct = dbg_chunks == nullptr ? nullptr : dbg_chunks + ((size_t)blockIdx.x * 512 + ((cc + j) & 511)) * 2;
     if (ct != nullptr && threadIdx.x == 0) ct[0] = wall_clock64();
 #endif
     if (!aborted) chunk_gemv4<B, K>(slot, min(RPC, rows - j * RPC), xsrc, [&](int i, const float* acc) { out(i, j, acc); });
+#if defined(MKD_TRACE_POLL) || defined(MKD_TRACE_BARRIER)
+    if (j == 0 && tr != nullptr && (threadIdx.x & 63) == 0)  // debug: first chunk computed
+      atomicMax(reinterpret_cast<unsigned long long*>(tr + 7), (unsigned long long)wall_clock64());
+#endif
 #ifdef MKD_TRACE_CHUNKS
     if (ct != nullptr && threadIdx.x == 0) ct[1] = wall_clock64();
 #endif
@@ -655,9 +666,9 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
     const uint64_t v = tw_make(pack_bf2(v0, v1), tag);
     const uint32_t off = ((uint32_t)r * (uint32_t)TW_GROUP + (uint32_t)b * STRIDE + (uint32_t)i) * 8u;
     uint64_t* q = reinterpret_cast<uint64_t*>(twb + off);
-    st_co(q, v);
+    st_tw(q, v);
   }
-  if (rw.q != nullptr) st_co(rw.q, rw.v);
+  if (rw.q != nullptr) st_tw(rw.q, rw.v);
 }
 static_assert(TW_WORDS * 8 < (1ull << 32), "tagged offsets are 32-bit");
 
@@ -997,10 +1008,10 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     if (split != nsplit - 1) {
       // read only by the last split of this (row, head)
       uint64_t* part = c.ws.tw(pbase + (size_t)split * PART_STRIDE);
-      st_co(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
+      st_tw(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
       if (dd == 0) {
-        st_co(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
-        st_co(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
+        st_tw(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
+        st_tw(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
       }
       c.sync();  // the scratch is reused by this workgroup's next task
       return true;
