@@ -334,7 +334,7 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
 #pragma unroll
   for (int b = 0; b < B; b++) {
     const float tot = c.red[b] + c.red[MAXB + b] + c.red[2 * MAXB + b] + c.red[3 * MAXB + b];
-    const float r = 1.0f / sqrtf(tot * (1.0f / H) + EPS);
+    const float r = __builtin_amdgcn_rsqf(tot * (1.0f / H) + EPS);  // v_rsq_f32 (1 ulp)
     // bf16(bf16(s * r) * w), pairwise through the packed conversion
     const uint32_t n01 = pack_bf2(s[b][0] * r, s[b][1] * r), n23 = pack_bf2(s[b][2] * r, s[b][3] * r);
     *reinterpret_cast<uint2*>(c.xs + (size_t)b * H + k0) =
@@ -653,7 +653,7 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
       for (int k = 0; k < 2; k++) {
         const float g = round_bf(c.res[(4 * i + 2 * k) * MAXB + b]);
         const float u = round_bf(c.res[(4 * i + 2 * k + 1) * MAXB + b]);
-        h[k] = g / (1.0f + expf(-g)) * u;
+        h[k] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;  // v_exp_f32, v_rcp_f32 (1 ulp each)
       }
       v0 = h[0]; v1 = h[1];
     } else if (OP == MKD_OP_DOWN) {  // rows arrive as two half-row partials
@@ -888,7 +888,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   if (wave < 3) {
     const float x0 = bf_lo(word), x1 = bf_hi(word);
     const float ss = wave_sum(x0 * x0 + x1 * x1);
-    const float r = 1.0f / sqrtf(ss * (1.0f / HD) + EPS);
+    const float r = __builtin_amdgcn_rsqf(ss * (1.0f / HD) + EPS);
     const float n0 = round_bf(round_bf(x0 * r) * bf_lo(wnw));
     const float n1 = round_bf(round_bf(x1 * r) * bf_hi(wnw));
     // rotate-half RoPE pairs dims i and i + 64: lane L holds 2L, 2L+1, lane L^32 the partners.
