@@ -822,6 +822,12 @@ __device__ __forceinline__ int p4_attn_chunks(const MkdStepDesc& d, const Inst& 
   return attn_geo(d.rows, b, pos_in, d.page_stride, d.block_size, w.a1, w.a2).nch;
 }
 
+// Softmax in base 2: scores scaled by hd^-0.5 * log2(e), so that every
+// exponential is one v_exp_f32 (2^x, 1 ulp); maxima and partial log-sums
+// (the split partials included) are in the same base-2 domain.
+constexpr float SCALE2 = ATTN_SCALE * 1.4426950408889634f;
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // ATTN task (row b, KV head h, split of nsplit of the row's positions).
 // The task's cached K/V arrive as KV chunks in the LDS ring (staged by the DMA
 // waves like weight rows), so the compute waves issue no cache loads of their
@@ -873,6 +879,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     c0 = cs[j]; c1 = cs[j + 1]; s0 = sn[j]; s1 = sn[j + 1];
   }
   const int blk_new = (split == 0 && active) ? table[pos / bs] : 0;
+  const int slot_in_blk = pos % bs;  // (integer division, off the poll's path)
   // this step's q (waves 0, 1: heads 2h, 2h+1), k (wave 2), v (wave 3): one word per lane
   size_t src;
   if (wave < 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + (size_t)(GROUP * h + wave) * (HD / 2) + lane;
@@ -911,7 +918,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     if (blk_new < 0 || blk_new >= nblk) {
       if (lane == 0) st_co(c.ws.line(CTR_ERR), ERR_BAD_INPUT);
     } else {
-      const size_t slotp = (size_t)blk_new * bs + pos % bs;
+      const size_t slotp = (size_t)blk_new * bs + slot_in_blk;
       uint16_t* cache = wave == 2 ? d.k_cache : d.v_cache;
       reinterpret_cast<uint32_t*>(cache + layer_off + slotp * KVS)[lane] = outw;
     }
@@ -920,7 +927,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   // the compiler sees unconsumed on some path stays pending in its view, and it
   // then waits for all memory operations (write-through stores included) before
   // that register is next written, in whatever task comes next.
-  asm volatile("" ::"v"(blk_new), "v"(wnw), "v"(c0), "v"(c1), "v"(s0), "v"(s1));
+  asm volatile("" ::"v"(blk_new), "v"(wnw), "v"(c0), "v"(c1), "v"(s0), "v"(s1), "v"(slot_in_blk));
   if (!p4_agree(c, ok)) {
     p4_skip_chunks<NS>(cc, nch);  // the DMA waves still hand the chunks over
     return false;
@@ -947,12 +954,12 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     float sc0 = sum_within_8(dot8(k1, qa[1], dot8(k0, qa[0], 0.f)));
     float sc1 = sum_within_8(dot8(k1, qc[1], dot8(k0, qc[0], 0.f)));
     const bool valid = p_begin + KV_CHUNK * j + pp < c_end;
-    sc0 = valid ? sc0 * ATTN_SCALE : -INFINITY;
-    sc1 = valid ? sc1 * ATTN_SCALE : -INFINITY;
+    sc0 = valid ? sc0 * SCALE2 : -INFINITY;
+    sc1 = valid ? sc1 * SCALE2 : -INFINITY;
     const float n0 = fmaxf(m0, max_over_8_groups(sc0)), n1 = fmaxf(m1, max_over_8_groups(sc1));
     // (a wave whose positions are all past c_end keeps m = -inf, l = 0)
-    const float al0 = n0 == -INFINITY ? 1.f : expf(m0 - n0), al1 = n1 == -INFINITY ? 1.f : expf(m1 - n1);
-    const float e0 = valid ? expf(sc0 - n0) : 0.f, e1 = valid ? expf(sc1 - n1) : 0.f;
+    const float al0 = n0 == -INFINITY ? 1.f : ex2(m0 - n0), al1 = n1 == -INFINITY ? 1.f : ex2(m1 - n1);
+    const float e0 = valid ? ex2(sc0 - n0) : 0.f, e1 = valid ? ex2(sc1 - n1) : 0.f;
     l0 = l0 * al0 + sum_over_8_groups(e0);
     l1 = l1 * al1 + sum_over_8_groups(e1);
     m0 = n0; m1 = n1;
@@ -967,13 +974,14 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     slot += SLOT_BYTES;
     if (slot == ring_end) slot = ring;
   }
-  if (wave == 0 && p_begin <= pos && pos < p_end) {
+  // (wave 3: it has the fewest cached positions in the last chunk)
+  if (wave == PK_CW - 1 && p_begin <= pos && pos < p_end) {
     const uint32_t kw = reinterpret_cast<const uint32_t*>(kb)[lane];
-    const float t0s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb)[lane], 0.f)) * ATTN_SCALE;
-    const float t1s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb + HD)[lane], 0.f)) * ATTN_SCALE;
+    const float t0s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb)[lane], 0.f)) * SCALE2;
+    const float t1s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb + HD)[lane], 0.f)) * SCALE2;
     const float n0 = fmaxf(m0, t0s), n1 = fmaxf(m1, t1s);
-    const float al0 = expf(m0 - n0), al1 = expf(m1 - n1);
-    const float e0 = expf(t0s - n0), e1 = expf(t1s - n1);
+    const float al0 = ex2(m0 - n0), al1 = ex2(m1 - n1);
+    const float e0 = ex2(t0s - n0), e1 = ex2(t1s - n1);
     l0 = l0 * al0 + e0;
     l1 = l1 * al1 + e1;
     m0 = n0; m1 = n1;
@@ -998,7 +1006,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   if (M != -INFINITY) {
 #pragma unroll
     for (int ww = 0; ww < PK_CW; ww++) {
-      const float sc = expf(mrg_ml[ww * GROUP + g] - M);
+      const float sc = ex2(mrg_ml[ww * GROUP + g] - M);
       num += mrg[(ww * GROUP + g) * HD + dd] * sc;
       den += mrg_ml[PK_CW * GROUP + ww * GROUP + g] * sc;
     }
@@ -1029,7 +1037,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
       const float ls = __uint_as_float((uint32_t)e[2]);
       if (ms == -INFINITY) continue;
       const float nm = fmaxf(M, ms);
-      const float sa = M == -INFINITY ? 0.f : expf(M - nm), sb = expf(ms - nm);
+      const float sa = M == -INFINITY ? 0.f : ex2(M - nm), sb = ex2(ms - nm);
       num = num * sa + ns * sb;
       den = den * sa + ls * sb;
       M = nm;
