@@ -817,7 +817,7 @@ __device__ __forceinline__ void p4_skip_chunks(int cc, int nch) {
 }
 // KV chunk count of an ATTN task (as the DMA waves compute it).
 __device__ __forceinline__ int p4_attn_chunks(const MkdStepDesc& d, const Inst& w) {
-  const int b = w.a0 / NKV;
+  const int b = (w.a0 & 63) / NKV;  // (a0 = b * 8 + h plus query-head flags from bit 6)
   const int pos_in = b < d.rows ? as_const(d.cache_seqlens)[b] : 0;
   return attn_geo(d.rows, b, pos_in, d.page_stride, d.block_size, w.a1, w.a2).nch;
 }
@@ -828,28 +828,35 @@ __device__ __forceinline__ int p4_attn_chunks(const MkdStepDesc& d, const Inst& 
 constexpr float SCALE2 = ATTN_SCALE * 1.4426950408889634f;
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// ATTN task (row b, KV head h, split of nsplit of the row's positions).
+// ATTN task of the tagged kernel: row b, KV head h, query head 2h + g, split
+// `split` of nsplit of the row's positions. Task word a0 = b * 8 + h, plus
+// ATTN_ONE_HEAD and g * ATTN_QHEAD; the two query heads of a KV head are
+// separate tasks (on two workgroups of the KV head's XCD), which halves each
+// task's chain of dependent instructions.
 // The task's cached K/V arrive as KV chunks in the LDS ring (staged by the DMA
 // waves like weight rows), so the compute waves issue no cache loads of their
 // own: their only global loads before the q/k/v poll are the norm weights and
 // the RoPE row, issued first, and the poll's rounds queue behind nothing else.
-// After the poll: q/k RMSNorm + RoPE in registers, the new token's K/V written
-// to its cache slot (split 0 of an active row) straight from registers, then
-// online softmax over the chunks, each chunk's 32 positions split over the four
-// waves (wave w: positions 8w .. 8w + 7):
+// After the poll (wave 0: q, wave 1: k, wave 2: v): q/k RMSNorm + RoPE in
+// registers, the new token's K/V written to its cache slot (by the g = 0 task,
+// split 0, of an active row) straight from registers, then online softmax over
+// the chunks, each chunk's 32 positions split over the four waves (wave w:
+// positions 8w .. 8w + 7):
 //   scores: lane (position p = lane >> 3, dims 16 (lane & 7) ..) dots 16 dims of
-//           K with both q heads, summed over the 8 lanes of the position;
+//           K with q, summed over the 8 lanes of the position;
 //   P * V:  lane (dims 2 lane, 2 lane + 1) over the wave's 8 positions, with the
 //           probabilities read from the lanes that hold them.
 // The four waves are merged at the end; the token's own K/V (not yet in the
 // cache when this task reads it) comes from LDS. The last split folds in the
 // other splits' tagged partials. nch returns the task's KV chunk count.
+constexpr int ATTN_QHEAD = 64, ATTN_ONE_HEAD = 128;  // task word a0 flags (b * 8 + h < 64)
 template <int B, int NS>
-__device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int bh, int split, int nsplit,
+__device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int a0, int split, int nsplit,
                                         uint64_t* tr, uint8_t* ring, int cc, int& nch) {
   const int t = p4_tid(), wave = t >> 6, lane = t & 63;
   const uint32_t tag = p4_tag(c.epoch, layer);
-  const int b = bh / NKV, h = bh % NKV;
+  const int bh = a0 & (ATTN_QHEAD - 1), g = (a0 & ATTN_QHEAD) ? 1 : 0;
+  const int b = bh / NKV, h = bh % NKV, qh = GROUP * h + g;
   const int bs = d.block_size;
   const int pos_in = b < d.rows ? as_const(d.cache_seqlens)[b] : 0;
   const AttnGeo ag = attn_geo(d.rows, b, pos_in, d.page_stride, bs, split, nsplit);
@@ -857,42 +864,44 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   if (b < d.rows && !ag.live && t == 0) st_co(c.ws.line(CTR_ERR), ERR_BAD_INPUT);
   const int pos = ag.pos, p_begin = ag.p_begin, p_end = ag.p_end, c_end = ag.c_end;
   const bool active = ag.live && as_const(d.row_active)[b] != 0;
+  const bool writes_kv = g == 0 && split == 0 && active;  // one task stores the new token's K/V
   cint32_t* table = as_const(d.page_table + (size_t)b * d.page_stride);
   const int nblk = d.num_blocks;
   uint8_t* smem = c.attn_smem;
-  uint16_t* qb = reinterpret_cast<uint16_t*>(smem);       // [2][128] roped q
-  uint16_t* kb = qb + GROUP * HD;                         // [128] roped k
+  uint16_t* qb = reinterpret_cast<uint16_t*>(smem);       // [128] roped q
+  uint16_t* kb = qb + HD;                                 // [128] roped k
   uint16_t* vb = kb + HD;                                 // [128] v
-  float* mrg = reinterpret_cast<float*>(smem + 1024);     // [4 waves][2][128]
-  float* mrg_ml = mrg + PK_CW * GROUP * HD;               // [4][2] m, [4][2] l
+  float* mrg = reinterpret_cast<float*>(smem + 1024);     // [4 waves][128]
+  float* mrg_ml = mrg + PK_CW * HD;                       // [4] m, [4] l
   const size_t layer_off = (size_t)layer * (size_t)d.kv_layer_stride + (size_t)h * HD;
 
   // static operands of the norm/RoPE step and the new token's cache slot: loaded
   // before the poll (the poll's first check then also covers them)
   uint32_t wnw = 0;
   float c0 = 0.f, c1 = 0.f, s0 = 0.f, s1 = 0.f;
-  if (wave < 3) {
-    wnw = ldg(reinterpret_cast<const uint32_t*>(p4_wptr(d, layer, wave < 2 ? MKD_W_Q_NORM : MKD_W_K_NORM)) + lane);
+  if (wave < 2) {
+    wnw = ldg(reinterpret_cast<const uint32_t*>(p4_wptr(d, layer, wave == 0 ? MKD_W_Q_NORM : MKD_W_K_NORM)) + lane);
     const int j = (2 * lane) & 63;
     const float* cs = d.rope_cos + (size_t)pos * (HD / 2);
     const float* sn = d.rope_sin + (size_t)pos * (HD / 2);
     c0 = cs[j]; c1 = cs[j + 1]; s0 = sn[j]; s1 = sn[j + 1];
   }
-  const int blk_new = (split == 0 && active) ? table[pos / bs] : 0;
+  const int blk_new = writes_kv ? table[pos / bs] : 0;
   const int slot_in_blk = pos % bs;  // (integer division, off the poll's path)
-  // this step's q (waves 0, 1: heads 2h, 2h+1), k (wave 2), v (wave 3): one word per lane
-  size_t src;
-  if (wave < 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + (size_t)(GROUP * h + wave) * (HD / 2) + lane;
-  else if (wave == 2) src = TW_QKV + (size_t)b * (QKV_N / 2) + QS / 2 + (size_t)h * (HD / 2) + lane;
-  else src = TW_QKV + (size_t)b * (QKV_N / 2) + (QS + KVS) / 2 + (size_t)h * (HD / 2) + lane;
-  uint64_t qv[1];
-  bool ok = poll_tagged<1>([=](int) { return c.ws.tw(src); }, qv, tag, c.ws);
+  // this step's q (wave 0: head qh), k (wave 1), v (wave 2): one word per lane
+  size_t src = TW_QKV + (size_t)b * (QKV_N / 2) + lane;
+  if (wave == 0) src += (size_t)qh * (HD / 2);
+  else if (wave == 1) src += QS / 2 + (size_t)h * (HD / 2);
+  else src += (QS + KVS) / 2 + (size_t)h * (HD / 2);
+  uint64_t qv[1] = {0};
+  bool ok = true;
+  if (wave < 3) ok = poll_tagged<1>([=](int) { return c.ws.tw(src); }, qv, tag, c.ws);
 #ifdef MKD_TRACE_POLL
-  if (tr != nullptr && lane == 0) atomicMax(reinterpret_cast<unsigned long long*>(tr + 1), (unsigned long long)wall_clock64());
+  if (tr != nullptr && lane == 0 && wave < 3) atomicMax(reinterpret_cast<unsigned long long*>(tr + 1), (unsigned long long)wall_clock64());
 #endif
   const uint32_t word = (uint32_t)qv[0];  // dims 2*lane, 2*lane + 1
   uint32_t outw = word;
-  if (wave < 3) {
+  if (wave < 2) {
     const float x0 = bf_lo(word), x1 = bf_hi(word);
     const float ss = wave_sum(x0 * x0 + x1 * x1);
     const float r = __builtin_amdgcn_rsqf(ss * (1.0f / HD) + EPS);
@@ -911,15 +920,14 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     outw = pack_bf2(o0, o1);
   }
   p4_trace_at(c, 4);
-  uint16_t* dst = wave < 2 ? qb + wave * HD : (wave == 2 ? kb : vb);
-  reinterpret_cast<uint32_t*>(dst)[lane] = outw;
-  // the new token's K (wave 2) and V (wave 3) go to their cache slot from registers
-  if (split == 0 && active && wave >= 2) {
+  if (wave < 3) reinterpret_cast<uint32_t*>(wave == 0 ? qb : (wave == 1 ? kb : vb))[lane] = outw;
+  // the new token's K (wave 1) and V (wave 2) go to their cache slot from registers
+  if (writes_kv && (wave == 1 || wave == 2)) {
     if (blk_new < 0 || blk_new >= nblk) {
       if (lane == 0) st_co(c.ws.line(CTR_ERR), ERR_BAD_INPUT);
     } else {
       const size_t slotp = (size_t)blk_new * bs + slot_in_blk;
-      uint16_t* cache = wave == 2 ? d.k_cache : d.v_cache;
+      uint16_t* cache = wave == 1 ? d.k_cache : d.v_cache;
       reinterpret_cast<uint32_t*>(cache + layer_off + slotp * KVS)[lane] = outw;
     }
   }
@@ -927,23 +935,20 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   // the compiler sees unconsumed on some path stays pending in its view, and it
   // then waits for all memory operations (write-through stores included) before
   // that register is next written, in whatever task comes next.
-  asm volatile("" ::"v"(blk_new), "v"(wnw), "v"(c0), "v"(c1), "v"(s0), "v"(s1), "v"(slot_in_blk));
+  asm volatile("" ::"v"(blk_new), "v"(wnw), "v"(c0), "v"(c1), "v"(s0), "v"(s1), "v"(slot_in_blk), "v"(word));
   if (!p4_agree(c, ok)) {
     p4_skip_chunks<NS>(cc, nch);  // the DMA waves still hand the chunks over
     return false;
   }
   if (tr != nullptr && t == 0) tr[2] = wall_clock64();
 
-  // scores layout: this lane's 16 dims of both q heads
+  // scores layout: this lane's 16 dims of q
   const int pl = lane >> 3, part = lane & 7;
-  uint4 qa[2], qc[2];
+  uint4 qa[2];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    qa[i] = reinterpret_cast<const uint4*>(qb + part * 16)[i];
-    qc[i] = reinterpret_cast<const uint4*>(qb + HD + part * 16)[i];
-  }
-  float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.f, l1 = 0.f;
-  float a00 = 0.f, a01 = 0.f, a10 = 0.f, a11 = 0.f;  // head g, dim 2 lane + i
+  for (int i = 0; i < 2; i++) qa[i] = reinterpret_cast<const uint4*>(qb + part * 16)[i];
+  float m0 = -INFINITY, l0 = 0.f;
+  float a00 = 0.f, a01 = 0.f;  // dims 2 lane, 2 lane + 1
   const uint8_t* slot = ring + (cc % NS) * SLOT_BYTES;
   const uint8_t* const ring_end = ring + NS * SLOT_BYTES;
   const int pp = 8 * wave + pl;  // this lane's position within a chunk
@@ -952,74 +957,64 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     const uint4 k0 = *reinterpret_cast<const uint4*>(slot + kv_kpiece(pp, 2 * part));
     const uint4 k1 = *reinterpret_cast<const uint4*>(slot + kv_kpiece(pp, 2 * part + 1));
     float sc0 = sum_within_8(dot8(k1, qa[1], dot8(k0, qa[0], 0.f)));
-    float sc1 = sum_within_8(dot8(k1, qc[1], dot8(k0, qc[0], 0.f)));
     const bool valid = p_begin + KV_CHUNK * j + pp < c_end;
     sc0 = valid ? sc0 * SCALE2 : -INFINITY;
-    sc1 = valid ? sc1 * SCALE2 : -INFINITY;
-    const float n0 = fmaxf(m0, max_over_8_groups(sc0)), n1 = fmaxf(m1, max_over_8_groups(sc1));
+    const float n0 = fmaxf(m0, max_over_8_groups(sc0));
     // (a wave whose positions are all past c_end keeps m = -inf, l = 0)
-    const float al0 = n0 == -INFINITY ? 1.f : ex2(m0 - n0), al1 = n1 == -INFINITY ? 1.f : ex2(m1 - n1);
-    const float e0 = valid ? ex2(sc0 - n0) : 0.f, e1 = valid ? ex2(sc1 - n1) : 0.f;
+    const float al0 = n0 == -INFINITY ? 1.f : ex2(m0 - n0);
+    const float e0 = valid ? ex2(sc0 - n0) : 0.f;
     l0 = l0 * al0 + sum_over_8_groups(e0);
-    l1 = l1 * al1 + sum_over_8_groups(e1);
-    m0 = n0; m1 = n1;
-    a00 *= al0; a01 *= al0; a10 *= al1; a11 *= al1;
+    m0 = n0;
+    a00 *= al0; a01 *= al0;
 #pragma unroll
     for (int q = 0; q < 8; q++) {
-      const float w0 = lane_value(e0, 8 * q), w1 = lane_value(e1, 8 * q);
+      const float w0 = lane_value(e0, 8 * q);
       const uint32_t vw = *reinterpret_cast<const uint32_t*>(slot + KV_V_OFF + (8 * wave + q) * 256 + 4 * lane);
       a00 += w0 * bf_lo(vw); a01 += w0 * bf_hi(vw);
-      a10 += w1 * bf_lo(vw); a11 += w1 * bf_hi(vw);
     }
     slot += SLOT_BYTES;
     if (slot == ring_end) slot = ring;
   }
-  // (wave 3: it has the fewest cached positions in the last chunk)
+  // the token's own position (wave 3: it has the fewest cached positions in the last chunk)
   if (wave == PK_CW - 1 && p_begin <= pos && pos < p_end) {
     const uint32_t kw = reinterpret_cast<const uint32_t*>(kb)[lane];
     const float t0s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb)[lane], 0.f)) * SCALE2;
-    const float t1s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb + HD)[lane], 0.f)) * SCALE2;
-    const float n0 = fmaxf(m0, t0s), n1 = fmaxf(m1, t1s);
-    const float al0 = ex2(m0 - n0), al1 = ex2(m1 - n1);
-    const float e0 = ex2(t0s - n0), e1 = ex2(t1s - n1);
+    const float n0 = fmaxf(m0, t0s);
+    const float al0 = ex2(m0 - n0), e0 = ex2(t0s - n0);
     l0 = l0 * al0 + e0;
-    l1 = l1 * al1 + e1;
-    m0 = n0; m1 = n1;
+    m0 = n0;
     const uint32_t vw = reinterpret_cast<const uint32_t*>(vb)[lane];
     a00 = a00 * al0 + e0 * bf_lo(vw); a01 = a01 * al0 + e0 * bf_hi(vw);
-    a10 = a10 * al1 + e1 * bf_lo(vw); a11 = a11 * al1 + e1 * bf_hi(vw);
   }
   // merge the waves in LDS
-  reinterpret_cast<float2*>(mrg + (wave * GROUP + 0) * HD)[lane] = make_float2(a00, a01);
-  reinterpret_cast<float2*>(mrg + (wave * GROUP + 1) * HD)[lane] = make_float2(a10, a11);
-  if (lane == 0) {
-    mrg_ml[wave * GROUP + 0] = m0; mrg_ml[wave * GROUP + 1] = m1;
-    mrg_ml[PK_CW * GROUP + wave * GROUP + 0] = l0; mrg_ml[PK_CW * GROUP + wave * GROUP + 1] = l1;
-  }
+  reinterpret_cast<float2*>(mrg + wave * HD)[lane] = make_float2(a00, a01);
+  if (lane == 0) { mrg_ml[wave] = m0; mrg_ml[PK_CW + wave] = l0; }
   c.sync();
-  // thread t = (g, dd): head 2h + g, dim dd
-  const int g = t >> 7, dd = t & 127;
+  // thread t: dim dd of the head; threads t and t + 128 compute the same value
+  const int dd = t & (HD - 1), half = t >> 7;
   float M = -INFINITY;
 #pragma unroll
-  for (int ww = 0; ww < PK_CW; ww++) M = fmaxf(M, mrg_ml[ww * GROUP + g]);
+  for (int ww = 0; ww < PK_CW; ww++) M = fmaxf(M, mrg_ml[ww]);
   float num = 0.f, den = 0.f;
   if (M != -INFINITY) {
 #pragma unroll
     for (int ww = 0; ww < PK_CW; ww++) {
-      const float sc = ex2(mrg_ml[ww * GROUP + g] - M);
-      num += mrg[(ww * GROUP + g) * HD + dd] * sc;
-      den += mrg_ml[PK_CW * GROUP + ww * GROUP + g] * sc;
+      const float sc = ex2(mrg_ml[ww] - M);
+      num += mrg[ww * HD + dd] * sc;
+      den += mrg_ml[PK_CW + ww] * sc;
     }
   }
   if (nsplit > 1) {
     const size_t pbase = TW_APART + (((size_t)b * NKV + h) * MAXS) * PART_STRIDE;
     if (split != nsplit - 1) {
-      // read only by the last split of this (row, head)
+      // read only by the last split of this (row, query head)
       uint64_t* part = c.ws.tw(pbase + (size_t)split * PART_STRIDE);
-      st_tw(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
-      if (dd == 0) {
-        st_tw(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
-        st_tw(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
+      if (half == 0) {
+        st_tw(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
+        if (dd == 0) {
+          st_tw(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
+          st_tw(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
+        }
       }
       c.sync();  // the scratch is reused by this workgroup's next task
       return true;
@@ -1046,11 +1041,13 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   const uint32_t mine = f2bf(num / den);
   const uint32_t nbr = __shfl_xor(mine, 1, 64);
   {
-    // the pair (dd, dd + 1) as one word; the even lane stores replicas 0-3, the odd one 4-7
+    // the pair (dd, dd + 1) as one word; its 8 replicas are stored by the four
+    // threads (dd even / odd, half 0 / 1) that hold it, two each
     const uint64_t v = tw_make((dd & 1) ? (nbr | (mine << 16)) : (mine | (nbr << 16)), tag);
-    const size_t word = TW_ATTN + (size_t)b * (QS / 2) + ((GROUP * h + g) * HD + dd) / 2;
+    const size_t word = TW_ATTN + (size_t)b * (QS / 2) + ((size_t)qh * HD + dd) / 2;
+    const int r0 = ((dd & 1) * 2 + half) * (TW_NREP / 4);
 #pragma unroll
-    for (int r = 0; r < TW_NREP / 2; r++) st_rep(c.ws, word, (dd & 1) * (TW_NREP / 2) + r, v);
+    for (int r = 0; r < TW_NREP / 4; r++) st_rep(c.ws, word, r0 + r, v);
   }
   return p4_agree(c, ok);  // also frees the scratch for the next task
 }
@@ -1100,7 +1097,7 @@ __device__ __forceinline__ T karg_field(const uint8_t* karg, size_t off) {
   return *reinterpret_cast<ct*>(reinterpret_cast<uintptr_t>(karg) + off);
 }
 __device__ __forceinline__ void dma_decode_attn(DmaTask& t, const uint8_t* karg, const Inst& w) {
-  const int b = w.a0 / NKV, h = w.a0 % NKV;
+  const int b = (w.a0 & (ATTN_QHEAD - 1)) / NKV, h = w.a0 % NKV;
   const int rows = karg_field<int32_t>(karg, offsetof(MkdStepDesc, rows));
   const int bs = karg_field<int32_t>(karg, offsetof(MkdStepDesc, block_size));
   const int stride = karg_field<int32_t>(karg, offsetof(MkdStepDesc, page_stride));
@@ -1381,6 +1378,10 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
     if (w.op == MKD_OP_QKV || w.op == MKD_OP_GATEUP) c.par ^= 1;
     if (w.op == MKD_OP_ATTN) {
       int nkv = 0;
+      if (!aborted && !(w.a0 & ATTN_ONE_HEAD)) {  // a task of both query heads: not this kernel's schedule
+        if (threadIdx.x == 0) st_co(ws.line(CTR_ERR), ERR_BAD_INST);
+        aborted = true;
+      }
       if (!aborted) {
         aborted = !p4_attn<B, Cfg::NS>(d, c, w.layer, w.a0, w.a1, w.a2, tr, ring, cc, nkv);
       } else {

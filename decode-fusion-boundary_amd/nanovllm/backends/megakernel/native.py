@@ -20,6 +20,10 @@ MAX_LM_SLOTS = 1024
 LAYER_PTRS = 11
 TW_REPLICAS = 8          # replicas of the tagged buffers every workgroup reads (one per XCD)
 KV_CHUNK = 32            # positions per KV chunk the tagged kernel stages (block_size must be a multiple)
+# ATTN task word a0 = b * 8 + h; the tagged kernel runs one query head per task:
+# ATTN_ONE_HEAD set, and ATTN_QHEAD set for the second head (2h + 1) of KV head h
+ATTN_QHEAD = 64
+ATTN_ONE_HEAD = 128
 
 FLAG_ADVANCE = 1
 FLAG_ZERO_FANIN = 2

@@ -29,7 +29,7 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 
 from .native import (
-    INST_WORDS, MAX_BATCH, MAX_LM_SLOTS, MAX_SPLITS, OP_ATTN, OP_DOWN, OP_GATEUP,
+    ATTN_ONE_HEAD, ATTN_QHEAD, INST_WORDS, MAX_BATCH, MAX_LM_SLOTS, MAX_SPLITS, OP_ATTN, OP_DOWN, OP_GATEUP,
     OP_LMHEAD, OP_OPROJ, OP_QKV,
 )
 
@@ -190,7 +190,11 @@ def _qkv_segments():
 
 
 def build_stages(batch: int, attn_splits: int, num_wgs: int,
-                 num_layers: int = NUM_LAYERS) -> list[Stage]:
+                 num_layers: int = NUM_LAYERS, q_head_tasks: bool = False) -> list[Stage]:
+    """The step's stages in dependency order. ``q_head_tasks`` (the tagged
+    kernel's schedule) makes one ATTN task per query head instead of per KV
+    head: task word a0 = b * 8 + h + ATTN_ONE_HEAD (+ ATTN_QHEAD for head 2h + 1)."""
+
     if batch not in BATCH_BUCKETS:
         raise ValueError(f"batch bucket must be one of {BATCH_BUCKETS}; got {batch}")
     if not 1 <= attn_splits <= MAX_SPLITS:
@@ -213,16 +217,18 @@ def build_stages(batch: int, attn_splits: int, num_wgs: int,
                 per_head[h] += 1
         stages.append(qkv)
         attn = Stage(OP_ATTN, layer)
+        heads = ([ATTN_ONE_HEAD, ATTN_ONE_HEAD | ATTN_QHEAD] if q_head_tasks else [0])
         for b in range(batch):
             for h in range(NUM_KV_HEADS):
                 for s in range(attn_splits):
-                    attn.tasks.append(Task(OP_ATTN, layer, b * NUM_KV_HEADS + h, s, attn_splits,
-                                           fanin_qkv(layer, h), per_head[h], fanin_attn(layer)))
+                    for flags in heads:
+                        attn.tasks.append(Task(OP_ATTN, layer, b * NUM_KV_HEADS + h + flags, s, attn_splits,
+                                               fanin_qkv(layer, h), per_head[h], fanin_attn(layer)))
         stages.append(attn)
         oproj = Stage(OP_OPROJ, layer)
         for r0, n in split_pairs(0, HIDDEN, num_wgs):
             oproj.tasks.append(Task(OP_OPROJ, layer, r0, n, 0, fanin_attn(layer),
-                                    batch * NUM_KV_HEADS, fanin_oproj(layer)))
+                                    batch * NUM_KV_HEADS * len(heads), fanin_oproj(layer)))
         stages.append(oproj)
         gu = Stage(OP_GATEUP, layer)
         for c0, n in split_pairs(0, INTERMEDIATE, num_wgs):
@@ -312,13 +318,13 @@ def split_layers(num_layers: int, groups: int) -> list[tuple[int, int]]:
 
 
 def build_segments(batch: int, attn_splits: int, num_wgs: int, num_layers: int = NUM_LAYERS,
-                   groups: int = 1) -> list[Schedule]:
+                   groups: int = 1, q_head_tasks: bool = False) -> list[Schedule]:
     """One persistent launch per layer segment. Segment ``k`` holds the stages of
     its layers (the last one also the LM head); its first QKV stage waits on the
     previous segment's down counter, which the earlier launch already completed,
     and the final LM-head task clears every fan-in counter of the step."""
 
-    stages = build_stages(batch, attn_splits, num_wgs, num_layers)
+    stages = build_stages(batch, attn_splits, num_wgs, num_layers, q_head_tasks)
     out = []
     for start, end in split_layers(num_layers, groups):
         seg = [s for s in stages if start <= s.layer < end or (end == num_layers and s.op == OP_LMHEAD)]

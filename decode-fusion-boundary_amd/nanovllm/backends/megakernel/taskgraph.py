@@ -107,8 +107,8 @@ class _Geometry:
 def _check_tagged_preconditions(segs) -> None:
     """What the tagged-exchange kernel relies on: GEMV row blocks of even size at
     even offsets (a word carries two values of one task), at most 32 rows per
-    block (its result tile), and an LM-head task on every workgroup of the last
-    launch (the last LM slot advances the step counter once every workgroup has
+    block (its result tile), one query head per attention task, and an LM-head
+    task on every workgroup of the last launch (the last LM slot advances the step counter once every workgroup has
     read it)."""
 
     for seg in segs:
@@ -119,6 +119,8 @@ def _check_tagged_preconditions(segs) -> None:
                     rows = 2 * t.a1 if t.op in (native.OP_GATEUP, native.OP_DOWN) else t.a1
                     if t.a0 % 2 or t.a1 % 2 or rows > 32:
                         raise RuntimeError(f"task {t} does not fit the tagged exchange (even blocks of <= 32 rows)")
+                if t.op == native.OP_ATTN and not t.a0 & native.ATTN_ONE_HEAD:
+                    raise RuntimeError(f"task {t}: the tagged kernel runs one query head per attention task")
     last = segs[-1]
     if any(not any(t.op == native.OP_LMHEAD for t in row) for row in last.rows):
         raise RuntimeError("the tagged exchange needs an LM-head task on every workgroup")
@@ -222,12 +224,13 @@ class TaskGraphDecoder:
         geo = self._geometries.get(key)
         if geo is not None:
             return geo
-        segs = build_segments(batch, splits, self.grid, self.num_layers, self.fusion_groups)
+        tagged = bool(self._variant_flags & native.FLAG_PK_TAGGED)
+        segs = build_segments(batch, splits, self.grid, self.num_layers, self.fusion_groups, q_head_tasks=tagged)
         whole = build_schedule(batch, splits, self.grid, self.num_layers)
         errors = verify(whole)
         if errors:
             raise RuntimeError("task-graph schedule failed verification: " + "; ".join(errors[:3]))
-        if self._variant_flags & native.FLAG_PK_TAGGED:
+        if tagged:
             _check_tagged_preconditions(segs)
         persistent = []
         for seg in segs:

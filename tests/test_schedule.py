@@ -102,10 +102,31 @@ def test_buckets_and_auto_splits():
 @pytest.mark.parametrize("batch", [1, 2, 4, 8])
 @pytest.mark.parametrize("splits", [1, 4, 16])
 def test_tagged_exchange_preconditions_at_256_cus(batch, splits):
-    """Even GEMV row blocks of <= 32 rows and an LM task on every workgroup."""
+    """Even GEMV row blocks of <= 32 rows, one query head per attention task and
+    an LM task on every workgroup; the per-KV-head schedule is rejected."""
     from nanovllm.backends.megakernel.taskgraph import _check_tagged_preconditions
     for groups in (1, 4):
-        _check_tagged_preconditions(build_segments(batch, splits, 256, 28, groups))
+        _check_tagged_preconditions(build_segments(batch, splits, 256, 28, groups, q_head_tasks=True))
+    with pytest.raises(RuntimeError, match="one query head"):
+        _check_tagged_preconditions(build_segments(batch, splits, 256, 28, 1))
+
+
+def test_query_head_attention_tasks():
+    """The tagged schedule has two ATTN tasks per (row, KV head, split): query
+    heads 2h and 2h + 1, flagged in a0 and placed on the KV head's die."""
+    from nanovllm.backends.megakernel.schedule import task_kv_head
+    for batch, splits in ((1, 1), (8, 4)):
+        seg = build_segments(batch, splits, 256, 28, 1, q_head_tasks=True)[0]
+        per_layer = {}
+        for w, row in enumerate(seg.rows):
+            for t in row:
+                if t.op == native.OP_ATTN:
+                    assert t.a0 & native.ATTN_ONE_HEAD
+                    assert task_kv_head(t) % 8 == w % 8
+                    key = (t.layer, t.a0 & (native.ATTN_QHEAD - 1), t.a1)
+                    per_layer.setdefault(key, []).append(bool(t.a0 & native.ATTN_QHEAD))
+        assert len(per_layer) == 28 * batch * 8 * splits
+        assert all(sorted(v) == [False, True] for v in per_layer.values())
 
 
 def test_xcd_aware_placement_keeps_heads_on_their_die():
