@@ -172,6 +172,11 @@ __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_
                                             const Ws& ws) {
   static_assert(N <= 32, "pending mask");
   uint32_t pending = N == 32 ? ~0u : ((1u << N) - 1u);
+  // The device error word and the clock are read only by a poll that has
+  // already spun 62 rounds: the error word is loaded ahead of a round's polls
+  // and examined with their results, so no round waits for a load of its own
+  // beyond the polls (a poll that succeeds early costs nothing extra).
+  uint32_t err = 0u;
   uint64_t t0 = 0;
   for (uint32_t spin = 0;; spin++) {
     // Every word is examined on every round (one already seen keeps its value
@@ -181,17 +186,21 @@ __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_
 #pragma unroll
     for (int k = 0; k < N; k++)
       if (tw_tag(a[k]) == tag) { v[k] = a[k]; pending &= ~(1u << k); }
-    if (pending == 0u) return true;
-    if ((spin & 63u) == 0u) {
+    if (pending == 0u) {
+      asm volatile("" ::"v"(err));  // (loaded before the polls just examined)
+      return true;
+    }
+    if ((spin & 63u) == 63u) {
+      if (err != 0u) return false;
       const uint64_t now = wall_clock64();
-      if (spin == 0) t0 = now;
-      if (ld_co(ws.line(CTR_ERR)) != 0u) return false;
-      if (now - t0 > 400000000ull) {  // 4 s at 100 MHz
+      if (t0 == 0) t0 = now;
+      else if (now - t0 > 400000000ull) {  // 4 s at 100 MHz
         st_co(ws.line(CTR_ERR), ERR_TIMEOUT);
         return false;
       }
     }
     __builtin_amdgcn_s_sleep(1);
+    if ((spin & 63u) == 62u) err = ld_co(ws.line(CTR_ERR));
 #pragma unroll
     for (int k = 0; k < N; k++)
       if ((pending >> k) & 1u) a[k] = ld_co(addr(k));
