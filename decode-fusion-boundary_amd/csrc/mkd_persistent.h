@@ -34,9 +34,12 @@ constexpr int MAX_LDS = 163840;
 template <int B>
 struct PkCfg {
   static constexpr int XS_BYTES = B * I * 2;
-  static constexpr int NS = (MAX_LDS - XS_BYTES - PK_SCRATCH) / SLOT_BYTES;
+  // (batch 8: 4 KiB more for the tagged kernel's partial-sum tile; the ring
+  // keeps its 6 slots)
+  static constexpr int SCRATCH = B >= 8 ? PK_SCRATCH + 4096 : PK_SCRATCH;
+  static constexpr int NS = (MAX_LDS - XS_BYTES - SCRATCH) / SLOT_BYTES;
   static constexpr int D = NS - 2;
-  static constexpr int LDS_BYTES = NS * SLOT_BYTES + XS_BYTES + PK_SCRATCH;
+  static constexpr int LDS_BYTES = NS * SLOT_BYTES + XS_BYTES + SCRATCH;
   static_assert(D >= 2, "lookahead too small");
 };
 

@@ -39,7 +39,16 @@ constexpr int P4_SCR_RED = 128;      // float [4][MAXB] sums / LM (value, index)
 constexpr int P4_SCR_STAGE = 512;   // u32 [2 parities][2 owners][MAXB][2] residual words awaiting publication
 constexpr int P4_STAGE_WORDS = 2 * MAXB * 2;
 constexpr int P4_SCR_RES = 1024;     // float [P4_MAX_ROWS][MAXB] task results
-constexpr int P4_SCR_ATTN = 2048;    // attention scratch (6 KiB)
+constexpr int P4_SCR_ATTN = 2048;    // attention scratch (3 KiB used)
+// Activation rows of K = 1024 (H) in LDS are padded by 16 bytes (XS_H bf16 per
+// row), so that the MFMA GEMV's reads of 8 rows at one offset hit 8 different
+// bank groups.
+constexpr int XS_H = H + 8;
+// float [4 waves][32 rows][B] partial sums of the MFMA GEMV (batch >= 4),
+// after the attention scratch (batch 4: 2 KiB) or in the 4 KiB added at batch 8
+template <int B>
+constexpr int p4_scr_part() { return B >= 8 ? PK_SCRATCH : 5632; }
+static_assert(5632 + 4 * 32 * 4 * 4 <= PK_SCRATCH && P4_SCR_ATTN + 3104 <= 5632, "partial tile overlaps");
 static_assert(P4_SCR_RES + 4 * P4_MAX_ROWS * MAXB <= P4_SCR_ATTN, "result tile overlaps");
 
 static_assert(P4_SCR_RED + 2 * 4 * PK_CW * MAXB <= P4_SCR_STAGE && P4_SCR_STAGE + 4 * 2 * P4_STAGE_WORDS <= P4_SCR_RES,
@@ -130,6 +139,7 @@ struct P4 {
                     // task, behind that task's barriers.
   uint64_t* trp;    // this task's trace record (debug builds with MKD_TRACE_POLL)
   int task;         // index of the current task in this workgroup's row
+  float* part;      // [4 waves][32 rows][B] partial sums of the MFMA GEMV (batch >= 4)
 };
 
 #if defined(MKD_TRACE_POLL) || defined(MKD_TRACE_BARRIER)
@@ -346,7 +356,7 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
     const float r = __builtin_amdgcn_rsqf(tot * (1.0f / H) + EPS);  // v_rsq_f32 (1 ulp)
     // bf16(bf16(s * r) * w), pairwise through the packed conversion
     const uint32_t n01 = pack_bf2(s[b][0] * r, s[b][1] * r), n23 = pack_bf2(s[b][2] * r, s[b][3] * r);
-    *reinterpret_cast<uint2*>(c.xs + (size_t)b * H + k0) =
+    *reinterpret_cast<uint2*>(c.xs + (size_t)b * XS_H + k0) =
         make_uint2(pack_bf2(bf_lo(n01) * w4[0], bf_hi(n01) * w4[1]), pack_bf2(bf_lo(n23) * w4[2], bf_hi(n23) * w4[3]));
   }
   c.sync();
@@ -381,6 +391,50 @@ struct GemvShape {
   static constexpr int PARTS = K == 3072 ? 2 : 1;             // waves per row (K > 1024)
   static constexpr int CPL = K == 1024 ? 4 : K / PARTS / 512;  // operands (uint4) per lane
 };
+// K = 1024 weight rows in a ring slot: the DMA stores 16-byte piece q of row r
+// (r < 8 in its chunk; 64 pieces per 1-KiB half row) at position
+// (q - r) mod 64 of its half, so that reads of one piece of 8 rows hit 8
+// different bank groups. Index (in pieces) of logical piece q of row r:
+__device__ __forceinline__ int w1024_piece(int r, int q) { return (q & 64) + (((q & 63) - (r & 7)) & 63); }
+
+typedef __bf16 p4_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float p4_f32x4 __attribute__((ext_vector_type(4)));
+// K = 1024 chunk (8 weight rows) on the matrix cores, batch >= 4: wave w
+// multiplies K quarter [256w, 256w + 256) of all 8 rows with 8
+// v_mfma_f32_16x16x32_bf16 (A = the B activation rows, M = 16; B = the 8
+// weight rows, N = 16; rows beyond B and 8 repeat real ones and their results
+// are dropped). Lane l supplies row / column l % 16 and K elements
+// 8 (l / 16) .. + 7 of each 32-wide step; result lane l holds column l % 16,
+// rows 4 (l / 16) .. + 3. The wave's partial sums go to part[(w * 32 + row) * B + b]
+// (part offset by the chunk's first row); the store epilogue adds the four
+// waves' partials in a fixed order.
+template <int B>
+__device__ __forceinline__ void chunk_mfma1024(const uint8_t* slot, const uint4* x4, float* part) {
+  static_assert(B >= 4 && B <= 8, "MFMA GEMV for batch 4 and 8");
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = lane & 15, kg = lane >> 4, r = n & 7;
+  const uint4* wrow = reinterpret_cast<const uint4*>(slot + (size_t)r * (H * 2));
+  const uint4* xrow = x4 + (size_t)(n & (B - 1)) * (XS_H / 8);
+  uint4 wv[8], xv[8];
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    const int q = 32 * wave + 4 * s + kg;  // 8-element piece of K
+    wv[s] = wrow[w1024_piece(r, q)];
+    xv[s] = xrow[q];
+  }
+  p4_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 8; s++)
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(p4_bf16x8, xv[s]), __builtin_bit_cast(p4_bf16x8, wv[s]),
+                                                  acc, 0, 0, 0);
+  if (n < 8 && 4 * kg < B)
+    *reinterpret_cast<float4*>(part + (size_t)(wave * 32 + n) * B + 4 * kg) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+// Chunk-result sink of the MFMA GEMV (p4_chunks passes it the chunk's rows).
+struct PartSink {
+  float* part;
+};
+
 // X source: the activations in LDS (bf16 [B][K]). (Polling them straight into
 // registers instead, each wave all of its operands, measured slower: four
 // times the polling loads outweigh the staging copy and its barrier.)
@@ -389,7 +443,7 @@ struct XLds {
   const uint4* x4;
   __device__ __forceinline__ uint4 get(int b, int c) const {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if constexpr (K == 1024) return x4[b * (K / 8) + c * 32 + (lane & 31)];
+    if constexpr (K == 1024) return x4[b * (XS_H / 8) + c * 32 + (lane & 31)];
     constexpr int CPL = GemvShape<K>::CPL;
     return x4[b * (K / 8) + (wave % GemvShape<K>::PARTS) * (CPL * 64) + c * 64 + lane];
   }
@@ -398,11 +452,11 @@ template <int B, int K, class X, class Out>
 __device__ __forceinline__ void chunk_gemv4(const uint8_t* slot, int nr, const X& xsrc, Out out) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if constexpr (K == 1024) {
-    const int half = lane >> 5, l = lane & 31;
-    const uint4* w4 = reinterpret_cast<const uint4*>(slot + (size_t)(2 * wave + half) * (K * 2));
+    const int half = lane >> 5, l = lane & 31, row = 2 * wave + half;
+    const uint4* w4 = reinterpret_cast<const uint4*>(slot + (size_t)row * (K * 2));
     uint4 wv[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) wv[c] = w4[c * 32 + l];
+    for (int c = 0; c < 4; c++) wv[c] = w4[w1024_piece(row, c * 32 + l)];
     float acc[B];
 #pragma unroll
     for (int b = 0; b < B; b++) {
@@ -536,7 +590,11 @@ __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int ro
     uint64_t* ct = dbg_chunks == nullptr ? nullptr : dbg_chunks + ((size_t)blockIdx.x * 512 + ((cc + j) & 511)) * 2;
     if (ct != nullptr && threadIdx.x == 0) ct[0] = wall_clock64();
 #endif
-    if (!aborted) chunk_gemv4<B, K>(slot, min(RPC, rows - j * RPC), xsrc, [&](int i, const float* acc) { out(i, j, acc); });
+    if constexpr (std::is_same<Out, PartSink>::value) {
+      if (!aborted) chunk_mfma1024<B>(slot, xsrc.x4, out.part + (size_t)j * RPC * B);
+    } else {
+      if (!aborted) chunk_gemv4<B, K>(slot, min(RPC, rows - j * RPC), xsrc, [&](int i, const float* acc) { out(i, j, acc); });
+    }
 #if defined(MKD_TRACE_POLL) || defined(MKD_TRACE_BARRIER)
     if (j == 0 && tr != nullptr && (threadIdx.x & 63) == 0)  // debug: first chunk computed
       atomicMax(reinterpret_cast<unsigned long long*>(tr + 7), (unsigned long long)wall_clock64());
@@ -577,7 +635,10 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
   const uint4* x4 = reinterpret_cast<const uint4*>(c.xs);
   switch (w.op) {
     case MKD_OP_QKV:
-    case MKD_OP_GATEUP: p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, to_res(8, 1), dbg); break;
+    case MKD_OP_GATEUP:
+      if constexpr (B >= 4) p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, PartSink{c.part}, dbg);
+      else p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, to_res(8, 1), dbg);
+      break;
     case MKD_OP_OPROJ: p4_chunks<B, QS, NS>(ring, cc, nch, rows, aborted, tr, XLds<QS>{x4}, to_res(4, 1), dbg); break;
     // DOWN: two half-row partials per row, result tile entries 2 * row + half
     case MKD_OP_DOWN: p4_chunks<B, I, NS>(ring, cc, nch, rows, aborted, tr, XLds<I>{x4}, to_res(2, 2), dbg); break;
@@ -656,12 +717,22 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
   for (int e = fo; e < n; e += PK_CW * 64) {
     const int r = e & ((1 << LR) - 1), b = (e >> LR) & (B - 1), i = e >> (LR + LB);
     float v0, v1;
+    // result of task row `row`, batch row b: one entry of the tile, or (MFMA
+    // GEMV) the four waves' partial sums, added in a fixed order
+    auto R = [&](int row) -> float {
+      if constexpr (B >= 4 && (OP == MKD_OP_QKV || OP == MKD_OP_GATEUP)) {
+        const float* p = c.part + (size_t)row * B + b;
+        return (p[0] + p[32 * B]) + (p[64 * B] + p[96 * B]);
+      } else {
+        return c.res[row * MAXB + b];
+      }
+    };
     if (OP == MKD_OP_GATEUP) {
       float h[2];
 #pragma unroll
       for (int k = 0; k < 2; k++) {
-        const float g = round_bf(c.res[(4 * i + 2 * k) * MAXB + b]);
-        const float u = round_bf(c.res[(4 * i + 2 * k + 1) * MAXB + b]);
+        const float g = round_bf(R(4 * i + 2 * k));
+        const float u = round_bf(R(4 * i + 2 * k + 1));
         h[k] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;  // v_exp_f32, v_rcp_f32 (1 ulp each)
       }
       v0 = h[0]; v1 = h[1];
@@ -669,8 +740,8 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
       v0 = c.res[(4 * i) * MAXB + b] + c.res[(4 * i + 1) * MAXB + b];
       v1 = c.res[(4 * i + 2) * MAXB + b] + c.res[(4 * i + 3) * MAXB + b];
     } else {
-      v0 = c.res[(2 * i) * MAXB + b];
-      v1 = c.res[(2 * i + 1) * MAXB + b];
+      v0 = R(2 * i);
+      v1 = R(2 * i + 1);
     }
     const uint64_t v = tw_make(pack_bf2(v0, v1), tag);
     const uint32_t off = ((uint32_t)r * (uint32_t)TW_GROUP + (uint32_t)b * STRIDE + (uint32_t)i) * 8u;
@@ -1218,11 +1289,16 @@ __device__ __forceinline__ void dma_issue(DmaTask& t, int j, uint8_t* slot, int 
   constexpr int LPW = UPC / 4;      // copies per DMA wave per chunk
   const int lane = threadIdx.x & 63;
 #ifndef MKD_PROBE_SKIP_DMA
+  // K = 1024: lane i of the copy of a half row brings piece (i + r) mod 64 of
+  // it, r = the row within the chunk (w1024_piece), a rotation per row
   if (j < t.nfull) {
 #pragma unroll
-    for (int k = 0; k < LPW; k++)
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)(t.src + k * t.kstep + lane * 8),
+    for (int k = 0; k < LPW; k++) {
+      // (full chunks: this wave's copy k is unit dw + 4k, row 2k + dw / 2)
+      const int src_lane = K == 1024 ? ((lane + 2 * k + (dw >> 1)) & 63) : lane;
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(t.src + k * t.kstep + src_lane * 8),
                                        (lds_void_t*)(slot + t.lds0 + k * t.ldsk), 16, 0, 0);
+    }
     t.src += t.cstep;
     return;
   }
@@ -1233,7 +1309,8 @@ __device__ __forceinline__ void dma_issue(DmaTask& t, int j, uint8_t* slot, int 
     const int r = u / PR, p = u - r * PR;
     const uint16_t* row = t.b1 != nullptr ? ((r & 1) ? t.b1 : t.b0) + (size_t)(r >> 1) * t.stride
                                           : t.b0 + (size_t)r * t.stride;
-    __builtin_amdgcn_global_load_lds((gbl_void_t*)(row + p * 512 + lane * 8), (lds_void_t*)(slot + (u - u0) * 1024),
+    const int src_lane = K == 1024 ? ((lane + ((u - u0) >> 1)) & 63) : lane;
+    __builtin_amdgcn_global_load_lds((gbl_void_t*)(row + p * 512 + src_lane * 8), (lds_void_t*)(slot + (u - u0) * 1024),
                                      16, 0, 0);
   }
 #else
@@ -1372,7 +1449,8 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
   }
   P4 c{ws, p4_xcc_id() % TW_NREP, (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch)}, flags,
              reinterpret_cast<float*>(scratch + P4_SCR_RED), reinterpret_cast<float*>(scratch + P4_SCR_RES), xs,
-             scratch + P4_SCR_ATTN, reinterpret_cast<uint32_t*>(scratch + P4_SCR_STAGE), 0, nullptr, 0};
+             scratch + P4_SCR_ATTN, reinterpret_cast<uint32_t*>(scratch + P4_SCR_STAGE), 0, nullptr, 0,
+             reinterpret_cast<float*>(scratch + p4_scr_part<B>())};
   bool aborted = false;
   int cc = 0;
   cint32_t* crow = as_const(row);
