@@ -435,6 +435,58 @@ struct PartSink {
   float* part;
 };
 
+// LM head on the matrix cores (batch >= 4): wave w takes the task's chunks
+// j = w, w + 4, ..., each whole (8 vocabulary rows x K = 1024: 32 MFMAs in two
+// accumulator chains), so no partial sums cross waves. Lane l (column n = l % 16,
+// row n % 8; result rows b = 4 (l / 16) + i) keeps a running greedy argmax of
+// its (row, b) logits: bf16-rounded value, then the lowest vocabulary index.
+struct LmLane {
+  float v[4];
+  int i[4];
+};
+struct LmSink {
+  LmLane* best;
+  uint16_t* logits;  // optional bf16 logits [batch rows][V]
+  int logit_rows;    // batch rows with logits
+  int row0, rows;    // first vocabulary row and row count of the task
+};
+template <int B>
+__device__ __forceinline__ void chunk_lm_mfma(const uint8_t* slot, const uint4* x4, int row, bool valid, LmLane& lb,
+                                              uint16_t* logits, int logit_rows) {
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, kg = lane >> 4, r = n & 7;
+  const uint4* wrow = reinterpret_cast<const uint4*>(slot + (size_t)r * (H * 2));
+  const uint4* xrow = x4 + (size_t)(n & (B - 1)) * (XS_H / 8);
+  p4_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s0 = 0; s0 < 32; s0 += 8) {
+    uint4 wv[8], xv[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+      const int q = 4 * (s0 + s) + kg;  // 8-element piece of K
+      wv[s] = wrow[w1024_piece(r, q)];
+      xv[s] = xrow[q];
+    }
+#pragma unroll
+    for (int s = 0; s < 8; s += 2) {
+      a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(p4_bf16x8, xv[s]), __builtin_bit_cast(p4_bf16x8, wv[s]),
+                                                   a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(p4_bf16x8, xv[s + 1]),
+                                                   __builtin_bit_cast(p4_bf16x8, wv[s + 1]), a1, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float acc = a0[i] + a1[i];
+    const float v = valid ? round_bf(acc) : -INFINITY;
+    const bool better = v > lb.v[i] || (v == lb.v[i] && row < lb.i[i]);
+    lb.v[i] = better ? v : lb.v[i];
+    lb.i[i] = better ? row : lb.i[i];
+    const int b = 4 * kg + i;
+    if (logits != nullptr && valid && n < 8 && b < B && b < logit_rows) logits[(size_t)b * V + row] = (uint16_t)f2bf(acc);
+  }
+}
+
 // X source: the activations in LDS (bf16 [B][K]). (Polling them straight into
 // registers instead, each wave all of its operands, measured slower: four
 // times the polling loads outweigh the staging copy and its barrier.)
@@ -592,6 +644,12 @@ __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int ro
 #endif
     if constexpr (std::is_same<Out, PartSink>::value) {
       if (!aborted) chunk_mfma1024<B>(slot, xsrc.x4, out.part + (size_t)j * RPC * B);
+    } else if constexpr (std::is_same<Out, LmSink>::value) {
+      // (every wave still takes each hand-over barrier above)
+      const int wave = threadIdx.x >> 6, r = (threadIdx.x & 15) & 7;
+      if (!aborted && (j & 3) == wave)
+        chunk_lm_mfma<B>(slot, xsrc.x4, out.row0 + j * RPC + r, j * RPC + r < out.rows, *out.best, out.logits,
+                         out.logit_rows);
     } else {
       if (!aborted) chunk_gemv4<B, K>(slot, min(RPC, rows - j * RPC), xsrc, [&](int i, const float* acc) { out(i, j, acc); });
     }
@@ -645,6 +703,33 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
     case MKD_OP_LMHEAD: {
       uint16_t* logits = d.out_logits;
       const int a0 = w.a0;
+      if constexpr (B >= 4) {
+        LmLane lb;
+#pragma unroll
+        for (int i = 0; i < 4; i++) { lb.v[i] = -INFINITY; lb.i[i] = 0x7fffffff; }
+        p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, LmSink{&lb, logits, d.rows, a0, rows}, dbg);
+        // per batch row b = 4 (l / 16) + i: (max, lowest index) over the 16 lanes
+        // of group l / 16, then broadcast from lane 16 (b / 4)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          float v = lb.v[i];
+          int ix = lb.i[i];
+#pragma unroll
+          for (int o = 1; o < 16; o <<= 1) {
+            const float v2 = __shfl_xor(v, o, 64);
+            const int i2 = __shfl_xor(ix, o, 64);
+            const bool better = v2 > v || (v2 == v && i2 < ix);
+            v = better ? v2 : v;
+            ix = better ? i2 : ix;
+          }
+#pragma unroll
+          for (int b = i; b < B; b += 4) {
+            best.v[b] = lane_value(v, 16 * (b / 4));
+            best.i[b] = __builtin_amdgcn_readlane(ix, 16 * (b / 4));
+          }
+        }
+        break;
+      }
       p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, [&](int r, int j, const float* acc) {
         const int row = a0 + j * 8 + r;
 #pragma unroll
