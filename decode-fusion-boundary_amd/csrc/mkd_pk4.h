@@ -40,12 +40,18 @@ constexpr int P4_SCR_STAGE = 512;   // u32 [2 parities][2 owners][MAXB][2] resid
 constexpr int P4_STAGE_WORDS = 2 * MAXB * 2;
 constexpr int P4_SCR_RES = 1024;     // float [P4_MAX_ROWS][MAXB] task results
 constexpr int P4_SCR_ATTN = 2048;    // attention scratch (3 KiB used)
+// Smallest batch bucket whose K = 1024 GEMVs (QKV, gate/up, LM head) run on
+// the matrix cores (smaller ones use v_dot2 chains).
+#ifndef MKD_MFMA_MIN_B
+#define MKD_MFMA_MIN_B 2
+#endif
+constexpr int MFMA_MIN_B = MKD_MFMA_MIN_B;
 // Activation rows of K = 1024 (H) in LDS are padded by 16 bytes (XS_H bf16 per
 // row), so that the MFMA GEMV's reads of 8 rows at one offset hit 8 different
 // bank groups.
 constexpr int XS_H = H + 8;
-// float [4 waves][32 rows][B] partial sums of the MFMA GEMV (batch >= 4),
-// after the attention scratch (batch 4: 2 KiB) or in the 4 KiB added at batch 8
+// float [4 waves][32 rows][B] partial sums of the MFMA GEMV (batch >= MFMA_MIN_B),
+// after the attention scratch (batch 2, 4: 1, 2 KiB) or in the 4 KiB added at batch 8
 template <int B>
 constexpr int p4_scr_part() { return B >= 8 ? PK_SCRATCH : 5632; }
 static_assert(5632 + 4 * 32 * 4 * 4 <= PK_SCRATCH && P4_SCR_ATTN + 3104 <= 5632, "partial tile overlaps");
@@ -139,7 +145,7 @@ struct P4 {
                     // task, behind that task's barriers.
   uint64_t* trp;    // this task's trace record (debug builds with MKD_TRACE_POLL)
   int task;         // index of the current task in this workgroup's row
-  float* part;      // [4 waves][32 rows][B] partial sums of the MFMA GEMV (batch >= 4)
+  float* part;      // [4 waves][32 rows][B] partial sums of the MFMA GEMV (batch >= MFMA_MIN_B)
 };
 
 #if defined(MKD_TRACE_POLL) || defined(MKD_TRACE_BARRIER)
@@ -399,7 +405,7 @@ __device__ __forceinline__ int w1024_piece(int r, int q) { return (q & 64) + (((
 
 typedef __bf16 p4_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float p4_f32x4 __attribute__((ext_vector_type(4)));
-// K = 1024 chunk (8 weight rows) on the matrix cores, batch >= 4: wave w
+// K = 1024 chunk (8 weight rows) on the matrix cores (batch >= MFMA_MIN_B): wave w
 // multiplies K quarter [256w, 256w + 256) of all 8 rows with 8
 // v_mfma_f32_16x16x32_bf16 (A = the B activation rows, M = 16; B = the 8
 // weight rows, N = 16; rows beyond B and 8 repeat real ones and their results
@@ -410,7 +416,7 @@ typedef float p4_f32x4 __attribute__((ext_vector_type(4)));
 // waves' partials in a fixed order.
 template <int B>
 __device__ __forceinline__ void chunk_mfma1024(const uint8_t* slot, const uint4* x4, float* part) {
-  static_assert(B >= 4 && B <= 8, "MFMA GEMV for batch 4 and 8");
+  static_assert(B >= 2 && B <= 8, "MFMA GEMV for batch 2 to 8");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = lane & 15, kg = lane >> 4, r = n & 7;
   const uint4* wrow = reinterpret_cast<const uint4*>(slot + (size_t)r * (H * 2));
@@ -427,15 +433,19 @@ __device__ __forceinline__ void chunk_mfma1024(const uint8_t* slot, const uint4*
   for (int s = 0; s < 8; s++)
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(p4_bf16x8, xv[s]), __builtin_bit_cast(p4_bf16x8, wv[s]),
                                                   acc, 0, 0, 0);
-  if (n < 8 && 4 * kg < B)
-    *reinterpret_cast<float4*>(part + (size_t)(wave * 32 + n) * B + 4 * kg) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  if constexpr (B >= 4) {
+    if (n < 8 && 4 * kg < B)
+      *reinterpret_cast<float4*>(part + (size_t)(wave * 32 + n) * B + 4 * kg) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  } else {
+    if (n < 8 && kg == 0) *reinterpret_cast<float2*>(part + (size_t)(wave * 32 + n) * B) = make_float2(acc[0], acc[1]);
+  }
 }
 // Chunk-result sink of the MFMA GEMV (p4_chunks passes it the chunk's rows).
 struct PartSink {
   float* part;
 };
 
-// LM head on the matrix cores (batch >= 4): wave w takes the task's chunks
+// LM head on the matrix cores (batch >= MFMA_MIN_B): wave w takes the task's chunks
 // j = w, w + 4, ..., each whole (8 vocabulary rows x K = 1024: 32 MFMAs in two
 // accumulator chains), so no partial sums cross waves. Lane l (column n = l % 16,
 // row n % 8; result rows b = 4 (l / 16) + i) keeps a running greedy argmax of
@@ -694,7 +704,7 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
   switch (w.op) {
     case MKD_OP_QKV:
     case MKD_OP_GATEUP:
-      if constexpr (B >= 4) p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, PartSink{c.part}, dbg);
+      if constexpr (B >= MFMA_MIN_B) p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, PartSink{c.part}, dbg);
       else p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, to_res(8, 1), dbg);
       break;
     case MKD_OP_OPROJ: p4_chunks<B, QS, NS>(ring, cc, nch, rows, aborted, tr, XLds<QS>{x4}, to_res(4, 1), dbg); break;
@@ -703,7 +713,7 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
     case MKD_OP_LMHEAD: {
       uint16_t* logits = d.out_logits;
       const int a0 = w.a0;
-      if constexpr (B >= 4) {
+      if constexpr (B >= MFMA_MIN_B) {
         LmLane lb;
 #pragma unroll
         for (int i = 0; i < 4; i++) { lb.v[i] = -INFINITY; lb.i[i] = 0x7fffffff; }
@@ -805,7 +815,7 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
     // result of task row `row`, batch row b: one entry of the tile, or (MFMA
     // GEMV) the four waves' partial sums, added in a fixed order
     auto R = [&](int row) -> float {
-      if constexpr (B >= 4 && (OP == MKD_OP_QKV || OP == MKD_OP_GATEUP)) {
+      if constexpr (B >= MFMA_MIN_B && (OP == MKD_OP_QKV || OP == MKD_OP_GATEUP)) {
         const float* p = c.part + (size_t)row * B + b;
         return (p[0] + p[32 * B]) + (p[64 * B] + p[96 * B]);
       } else {
