@@ -46,10 +46,20 @@ constexpr int P4_SCR_ATTN = 2048;    // attention scratch (3 KiB used)
 #define MKD_MFMA_MIN_B 2
 #endif
 constexpr int MFMA_MIN_B = MKD_MFMA_MIN_B;
+// The same for o_proj and down (K = 2048, 3072: 4 and 2 weight rows per chunk,
+// so a tile of 16 x 16 keeps less of its work; measured slower at batch 2).
+constexpr int MFMA_MIN_B_WIDE = 4;
+template <int B, int OP>
+constexpr bool p4_mfma_op() {
+  return OP == MKD_OP_OPROJ || OP == MKD_OP_DOWN ? B >= MFMA_MIN_B_WIDE : B >= MFMA_MIN_B;
+}
 // Activation rows of K = 1024 (H) in LDS are padded by 16 bytes (XS_H bf16 per
 // row), so that the MFMA GEMV's reads of 8 rows at one offset hit 8 different
 // bank groups.
 constexpr int XS_H = H + 8;
+// Activation rows of K = 2048 and 3072 are not padded (the batch-4 ring would
+// lose a slot): 16-byte piece q of row b is stored at piece q ^ (b mod 8).
+__device__ __forceinline__ int xs_piece(int b, int q) { return q ^ (b & 7); }
 // float [4 waves][32 rows][B] partial sums of the MFMA GEMV (batch >= MFMA_MIN_B),
 // after the attention scratch (batch 2, 4: 1, 2 KiB) or in the 4 KiB added at batch 8
 template <int B>
@@ -215,7 +225,10 @@ __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_
         return false;
       }
     }
-    __builtin_amdgcn_s_sleep(1);
+#ifndef MKD_POLL_SLEEP
+#define MKD_POLL_SLEEP 1
+#endif
+    __builtin_amdgcn_s_sleep(MKD_POLL_SLEEP);
     if ((spin & 63u) == 62u) err = ld_co(ws.line(CTR_ERR));
 #pragma unroll
     for (int k = 0; k < N; k++)
@@ -266,7 +279,13 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
     ok = ok && poll_tagged<NB>([&](int k) { return src + t + 256 * (k0 + k); }, v, tag, c.ws);
     if (k0 == 0) p4_trace_poll(c);
 #pragma unroll
-    for (int k = 0; k < NB; k++) dst[t + 256 * (k0 + k)] = (uint32_t)v[k];
+    for (int k = 0; k < NB; k++) {
+      // word t + 256 m of [B][K/2]: row m / WPR, word 256 (m % WPR) + t of it,
+      // its 16-byte piece XOR-swizzled by the row (xs_piece)
+      constexpr int WPR = K / 2 / 256;
+      const int m = k0 + k, b = m / WPR, ww = 256 * (m % WPR) + t;
+      dst[b * (K / 2) + xs_piece(b, ww >> 2) * 4 + (ww & 3)] = (uint32_t)v[k];
+    }
   }
   return p4_agree(c, ok);
 }
@@ -397,47 +416,58 @@ struct GemvShape {
   static constexpr int PARTS = K == 3072 ? 2 : 1;             // waves per row (K > 1024)
   static constexpr int CPL = K == 1024 ? 4 : K / PARTS / 512;  // operands (uint4) per lane
 };
-// K = 1024 weight rows in a ring slot: the DMA stores 16-byte piece q of row r
-// (r < 8 in its chunk; 64 pieces per 1-KiB half row) at position
-// (q - r) mod 64 of its half, so that reads of one piece of 8 rows hit 8
-// different bank groups. Index (in pieces) of logical piece q of row r:
-__device__ __forceinline__ int w1024_piece(int r, int q) { return (q & 64) + (((q & 63) - (r & 7)) & 63); }
+// Weight rows in a ring slot: the DMA stores 16-byte piece q of row r of its
+// chunk (64 pieces per 1-KiB unit) at position (q - r) mod 64 of its unit, so
+// that reads of one piece of up to 8 rows hit different bank groups. Index (in
+// pieces) of logical piece q of row r:
+__device__ __forceinline__ int wpiece(int r, int q) { return (q & ~63) + (((q & 63) - (r & 7)) & 63); }
 
 typedef __bf16 p4_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float p4_f32x4 __attribute__((ext_vector_type(4)));
-// K = 1024 chunk (8 weight rows) on the matrix cores (batch >= MFMA_MIN_B): wave w
-// multiplies K quarter [256w, 256w + 256) of all 8 rows with 8
-// v_mfma_f32_16x16x32_bf16 (A = the B activation rows, M = 16; B = the 8
-// weight rows, N = 16; rows beyond B and 8 repeat real ones and their results
-// are dropped). Lane l supplies row / column l % 16 and K elements
+// One chunk (RPC = 8 / 4 / 2 weight rows of K = 1024 / 2048 / 3072) on the
+// matrix cores (p4_mfma_op: batch >= 2, o_proj and down >= 4): wave w multiplies K quarter
+// [K w / 4, K (w + 1) / 4) of the chunk's rows with K / 128 v_mfma_f32_16x16x32_bf16
+// (A = the B activation rows, M = 16; B = the weight rows, N = 16; rows
+// beyond B and RPC repeat real ones and their results are dropped), in two
+// accumulator chains. Lane l supplies row / column l % 16 and K elements
 // 8 (l / 16) .. + 7 of each 32-wide step; result lane l holds column l % 16,
-// rows 4 (l / 16) .. + 3. The wave's partial sums go to part[(w * 32 + row) * B + b]
-// (part offset by the chunk's first row); the store epilogue adds the four
-// waves' partials in a fixed order.
-template <int B>
-__device__ __forceinline__ void chunk_mfma1024(const uint8_t* slot, const uint4* x4, float* part) {
+// rows 4 (l / 16) .. + 3. The wave's partial sums go to
+// part[(w * 32 + row) * B + b] (part offset by the chunk's first row); the
+// store epilogue adds the four waves' partials in a fixed order.
+template <int B, int K>
+__device__ __forceinline__ void chunk_mfma(const uint8_t* slot, const uint4* x4, float* part) {
   static_assert(B >= 2 && B <= 8, "MFMA GEMV for batch 2 to 8");
+  constexpr int RPC = K == 1024 ? 8 : (K == 2048 ? 4 : 2);
+  constexpr int STEPS = K / 128;      // 32-wide K steps per wave
+  constexpr int PPW = K / 32;         // 16-byte pieces per wave's K quarter
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n = lane & 15, kg = lane >> 4, r = n & 7;
-  const uint4* wrow = reinterpret_cast<const uint4*>(slot + (size_t)r * (H * 2));
-  const uint4* xrow = x4 + (size_t)(n & (B - 1)) * (XS_H / 8);
-  uint4 wv[8], xv[8];
+  const int n = lane & 15, kg = lane >> 4, r = n & (RPC - 1), b = n & (B - 1);
+  const uint4* wrow = reinterpret_cast<const uint4*>(slot + (size_t)r * (K * 2));
+  const uint4* xrow = x4 + (size_t)b * (K == 1024 ? XS_H / 8 : K / 8);
+  p4_f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < 8; s++) {
-    const int q = 32 * wave + 4 * s + kg;  // 8-element piece of K
-    wv[s] = wrow[w1024_piece(r, q)];
-    xv[s] = xrow[q];
+  for (int s0 = 0; s0 < STEPS; s0 += 8) {
+    uint4 wv[8], xv[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+      const int q = PPW * wave + 4 * (s0 + s) + kg;  // 8-element piece of K
+      wv[s] = wrow[wpiece(r, q)];
+      xv[s] = xrow[K == 1024 ? q : xs_piece(b, q)];
+    }
+#pragma unroll
+    for (int s = 0; s < 8; s += 2) {
+      a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(p4_bf16x8, xv[s]), __builtin_bit_cast(p4_bf16x8, wv[s]),
+                                                   a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(p4_bf16x8, xv[s + 1]),
+                                                   __builtin_bit_cast(p4_bf16x8, wv[s + 1]), a1, 0, 0, 0);
+    }
   }
-  p4_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < 8; s++)
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(p4_bf16x8, xv[s]), __builtin_bit_cast(p4_bf16x8, wv[s]),
-                                                  acc, 0, 0, 0);
+  const p4_f32x4 acc = a0 + a1;
   if constexpr (B >= 4) {
-    if (n < 8 && 4 * kg < B)
+    if (n < RPC && 4 * kg < B)
       *reinterpret_cast<float4*>(part + (size_t)(wave * 32 + n) * B + 4 * kg) = make_float4(acc[0], acc[1], acc[2], acc[3]);
   } else {
-    if (n < 8 && kg == 0) *reinterpret_cast<float2*>(part + (size_t)(wave * 32 + n) * B) = make_float2(acc[0], acc[1]);
+    if (n < RPC && kg == 0) *reinterpret_cast<float2*>(part + (size_t)(wave * 32 + n) * B) = make_float2(acc[0], acc[1]);
   }
 }
 // Chunk-result sink of the MFMA GEMV (p4_chunks passes it the chunk's rows).
@@ -474,7 +504,7 @@ __device__ __forceinline__ void chunk_lm_mfma(const uint8_t* slot, const uint4* 
 #pragma unroll
     for (int s = 0; s < 8; s++) {
       const int q = 4 * (s0 + s) + kg;  // 8-element piece of K
-      wv[s] = wrow[w1024_piece(r, q)];
+      wv[s] = wrow[wpiece(r, q)];
       xv[s] = xrow[q];
     }
 #pragma unroll
@@ -507,7 +537,7 @@ struct XLds {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if constexpr (K == 1024) return x4[b * (XS_H / 8) + c * 32 + (lane & 31)];
     constexpr int CPL = GemvShape<K>::CPL;
-    return x4[b * (K / 8) + (wave % GemvShape<K>::PARTS) * (CPL * 64) + c * 64 + lane];
+    return x4[b * (K / 8) + xs_piece(b, (wave % GemvShape<K>::PARTS) * (CPL * 64) + c * 64 + lane)];
   }
 };
 template <int B, int K, class X, class Out>
@@ -518,7 +548,7 @@ __device__ __forceinline__ void chunk_gemv4(const uint8_t* slot, int nr, const X
     const uint4* w4 = reinterpret_cast<const uint4*>(slot + (size_t)row * (K * 2));
     uint4 wv[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) wv[c] = w4[w1024_piece(row, c * 32 + l)];
+    for (int c = 0; c < 4; c++) wv[c] = w4[wpiece(row, c * 32 + l)];
     float acc[B];
 #pragma unroll
     for (int b = 0; b < B; b++) {
@@ -540,10 +570,10 @@ __device__ __forceinline__ void chunk_gemv4(const uint8_t* slot, int nr, const X
     constexpr int PARTS = K == 2048 ? 1 : 2;      // waves per row
     constexpr int CPL = K / PARTS / 512;          // uint4 per lane: 4 or 3
     const int row = wave / PARTS, part = wave % PARTS;
-    const uint4* w4 = reinterpret_cast<const uint4*>(slot + (size_t)row * (K * 2)) + part * (CPL * 64);
+    const uint4* w4 = reinterpret_cast<const uint4*>(slot + (size_t)row * (K * 2));
     uint4 wv[CPL];
 #pragma unroll
-    for (int c = 0; c < CPL; c++) wv[c] = w4[c * 64 + lane];
+    for (int c = 0; c < CPL; c++) wv[c] = w4[wpiece(row, part * (CPL * 64) + c * 64 + lane)];
     float acc[B];
 #pragma unroll
     for (int b = 0; b < B; b++) {
@@ -653,7 +683,7 @@ __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int ro
     if (ct != nullptr && threadIdx.x == 0) ct[0] = wall_clock64();
 #endif
     if constexpr (std::is_same<Out, PartSink>::value) {
-      if (!aborted) chunk_mfma1024<B>(slot, xsrc.x4, out.part + (size_t)j * RPC * B);
+      if (!aborted) chunk_mfma<B, K>(slot, xsrc.x4, out.part + (size_t)j * RPC * B);
     } else if constexpr (std::is_same<Out, LmSink>::value) {
       // (every wave still takes each hand-over barrier above)
       const int wave = threadIdx.x >> 6, r = (threadIdx.x & 15) & 7;
@@ -704,12 +734,18 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
   switch (w.op) {
     case MKD_OP_QKV:
     case MKD_OP_GATEUP:
-      if constexpr (B >= MFMA_MIN_B) p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, PartSink{c.part}, dbg);
+      if constexpr (p4_mfma_op<B, MKD_OP_QKV>()) p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, PartSink{c.part}, dbg);
       else p4_chunks<B, H, NS>(ring, cc, nch, rows, aborted, tr, XLds<H>{x4}, to_res(8, 1), dbg);
       break;
-    case MKD_OP_OPROJ: p4_chunks<B, QS, NS>(ring, cc, nch, rows, aborted, tr, XLds<QS>{x4}, to_res(4, 1), dbg); break;
-    // DOWN: two half-row partials per row, result tile entries 2 * row + half
-    case MKD_OP_DOWN: p4_chunks<B, I, NS>(ring, cc, nch, rows, aborted, tr, XLds<I>{x4}, to_res(2, 2), dbg); break;
+    case MKD_OP_OPROJ:
+      if constexpr (p4_mfma_op<B, MKD_OP_OPROJ>()) p4_chunks<B, QS, NS>(ring, cc, nch, rows, aborted, tr, XLds<QS>{x4}, PartSink{c.part}, dbg);
+      else p4_chunks<B, QS, NS>(ring, cc, nch, rows, aborted, tr, XLds<QS>{x4}, to_res(4, 1), dbg);
+      break;
+    // DOWN (v_dot2 chains): two half-row partials per row, result tile entries 2 * row + half
+    case MKD_OP_DOWN:
+      if constexpr (p4_mfma_op<B, MKD_OP_DOWN>()) p4_chunks<B, I, NS>(ring, cc, nch, rows, aborted, tr, XLds<I>{x4}, PartSink{c.part}, dbg);
+      else p4_chunks<B, I, NS>(ring, cc, nch, rows, aborted, tr, XLds<I>{x4}, to_res(2, 2), dbg);
+      break;
     case MKD_OP_LMHEAD: {
       uint16_t* logits = d.out_logits;
       const int a0 = w.a0;
@@ -815,7 +851,7 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
     // result of task row `row`, batch row b: one entry of the tile, or (MFMA
     // GEMV) the four waves' partial sums, added in a fixed order
     auto R = [&](int row) -> float {
-      if constexpr (B >= MFMA_MIN_B && (OP == MKD_OP_QKV || OP == MKD_OP_GATEUP)) {
+      if constexpr (p4_mfma_op<B, OP>()) {
         const float* p = c.part + (size_t)row * B + b;
         return (p[0] + p[32 * B]) + (p[64 * B] + p[96 * B]);
       } else {
@@ -831,7 +867,10 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
         h[k] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;  // v_exp_f32, v_rcp_f32 (1 ulp each)
       }
       v0 = h[0]; v1 = h[1];
-    } else if (OP == MKD_OP_DOWN) {  // rows arrive as two half-row partials
+    } else if (OP == MKD_OP_DOWN && p4_mfma_op<B, MKD_OP_DOWN>()) {
+      v0 = R(2 * i);
+      v1 = R(2 * i + 1);
+    } else if (OP == MKD_OP_DOWN) {  // (v_dot2 chains) rows arrive as two half-row partials
       v0 = c.res[(4 * i) * MAXB + b] + c.res[(4 * i + 1) * MAXB + b];
       v1 = c.res[(4 * i + 2) * MAXB + b] + c.res[(4 * i + 3) * MAXB + b];
     } else {
@@ -1384,13 +1423,15 @@ __device__ __forceinline__ void dma_issue(DmaTask& t, int j, uint8_t* slot, int 
   constexpr int LPW = UPC / 4;      // copies per DMA wave per chunk
   const int lane = threadIdx.x & 63;
 #ifndef MKD_PROBE_SKIP_DMA
-  // K = 1024: lane i of the copy of a half row brings piece (i + r) mod 64 of
-  // it, r = the row within the chunk (w1024_piece), a rotation per row
+  // lane i of the copy of a 1-KiB unit brings piece (i + r) mod 64 of it, r =
+  // the unit's row within the chunk (wpiece): a rotation per row
   if (j < t.nfull) {
 #pragma unroll
     for (int k = 0; k < LPW; k++) {
-      // (full chunks: this wave's copy k is unit dw + 4k, row 2k + dw / 2)
-      const int src_lane = K == 1024 ? ((lane + 2 * k + (dw >> 1)) & 63) : lane;
+      // (full chunks: this wave's copy k is unit dw + 4k, row 2k + dw / 2 at
+      // K = 1024 and row k at 2048; unit 3 dw + k, row dw / 2 at 3072)
+      const int r = K == 1024 ? 2 * k + (dw >> 1) : (K == 2048 ? k : dw >> 1);
+      const int src_lane = (lane + r) & 63;
       __builtin_amdgcn_global_load_lds((gbl_void_t*)(t.src + k * t.kstep + src_lane * 8),
                                        (lds_void_t*)(slot + t.lds0 + k * t.ldsk), 16, 0, 0);
     }
@@ -1404,7 +1445,7 @@ __device__ __forceinline__ void dma_issue(DmaTask& t, int j, uint8_t* slot, int 
     const int r = u / PR, p = u - r * PR;
     const uint16_t* row = t.b1 != nullptr ? ((r & 1) ? t.b1 : t.b0) + (size_t)(r >> 1) * t.stride
                                           : t.b0 + (size_t)r * t.stride;
-    const int src_lane = K == 1024 ? ((lane + ((u - u0) >> 1)) & 63) : lane;
+    const int src_lane = (lane + (u - u0) / PR) & 63;
     __builtin_amdgcn_global_load_lds((gbl_void_t*)(row + p * 512 + src_lane * 8), (lds_void_t*)(slot + (u - u0) * 1024),
                                      16, 0, 0);
   }
