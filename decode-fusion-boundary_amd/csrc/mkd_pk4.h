@@ -49,9 +49,14 @@ constexpr int MFMA_MIN_B = MKD_MFMA_MIN_B;
 // The same for o_proj and down (K = 2048, 3072: 4 and 2 weight rows per chunk,
 // so a tile of 16 x 16 keeps less of its work; measured slower at batch 2).
 constexpr int MFMA_MIN_B_WIDE = 4;
+#ifndef MKD_MFMA_MIN_B_LM
+#define MKD_MFMA_MIN_B_LM MKD_MFMA_MIN_B
+#endif
 template <int B, int OP>
 constexpr bool p4_mfma_op() {
-  return OP == MKD_OP_OPROJ || OP == MKD_OP_DOWN ? B >= MFMA_MIN_B_WIDE : B >= MFMA_MIN_B;
+  return OP == MKD_OP_OPROJ || OP == MKD_OP_DOWN ? B >= MFMA_MIN_B_WIDE
+         : OP == MKD_OP_LMHEAD                  ? B >= MKD_MFMA_MIN_B_LM
+                                                : B >= MFMA_MIN_B;
 }
 // Activation rows of K = 1024 (H) in LDS are padded by 16 bytes (XS_H bf16 per
 // row), so that the MFMA GEMV's reads of 8 rows at one offset hit 8 different
@@ -436,7 +441,7 @@ typedef float p4_f32x4 __attribute__((ext_vector_type(4)));
 // store epilogue adds the four waves' partials in a fixed order.
 template <int B, int K>
 __device__ __forceinline__ void chunk_mfma(const uint8_t* slot, const uint4* x4, float* part) {
-  static_assert(B >= 2 && B <= 8, "MFMA GEMV for batch 2 to 8");
+  static_assert(B >= 1 && B <= 8, "MFMA GEMV for batch 1 to 8");
   constexpr int RPC = K == 1024 ? 8 : (K == 2048 ? 4 : 2);
   constexpr int STEPS = K / 128;      // 32-wide K steps per wave
   constexpr int PPW = K / 32;         // 16-byte pieces per wave's K quarter
@@ -466,8 +471,10 @@ __device__ __forceinline__ void chunk_mfma(const uint8_t* slot, const uint4* x4,
   if constexpr (B >= 4) {
     if (n < RPC && 4 * kg < B)
       *reinterpret_cast<float4*>(part + (size_t)(wave * 32 + n) * B + 4 * kg) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  } else {
+  } else if constexpr (B == 2) {
     if (n < RPC && kg == 0) *reinterpret_cast<float2*>(part + (size_t)(wave * 32 + n) * B) = make_float2(acc[0], acc[1]);
+  } else {
+    if (n < RPC && kg == 0) part[(size_t)(wave * 32 + n) * B] = acc[0];
   }
 }
 // Chunk-result sink of the MFMA GEMV (p4_chunks passes it the chunk's rows).
@@ -749,7 +756,7 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
     case MKD_OP_LMHEAD: {
       uint16_t* logits = d.out_logits;
       const int a0 = w.a0;
-      if constexpr (B >= MFMA_MIN_B) {
+      if constexpr (p4_mfma_op<B, MKD_OP_LMHEAD>()) {
         LmLane lb;
 #pragma unroll
         for (int i = 0; i < 4; i++) { lb.v[i] = -INFINITY; lb.i[i] = 0x7fffffff; }
@@ -1161,7 +1168,14 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   uint4 qa[2];
 #pragma unroll
   for (int i = 0; i < 2; i++) qa[i] = reinterpret_cast<const uint4*>(qb + part * 16)[i];
-  float m0 = -INFINITY, l0 = 0.f;
+  // Online softmax with a lazily raised reference maximum m0: the
+  // probabilities are 2^(score - m0), and m0 (with the sums and the output
+  // accumulators) is rescaled only when a score exceeds it by more than
+  // LAZY_LOG2 (so every probability stays below 2^LAZY_LOG2). The sum of
+  // probabilities is kept per lane (the lanes with part 0, one per position)
+  // and reduced once after the loop.
+  constexpr float LAZY_LOG2 = 8.f;
+  float m0 = -INFINITY, ls = 0.f;
   float a00 = 0.f, a01 = 0.f;  // dims 2 lane, 2 lane + 1
   const uint8_t* slot = ring + (cc % NS) * SLOT_BYTES;
   const uint8_t* const ring_end = ring + NS * SLOT_BYTES;
@@ -1173,13 +1187,16 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     float sc0 = sum_within_8(dot8(k1, qa[1], dot8(k0, qa[0], 0.f)));
     const bool valid = p_begin + KV_CHUNK * j + pp < c_end;
     sc0 = valid ? sc0 * SCALE2 : -INFINITY;
-    const float n0 = fmaxf(m0, max_over_8_groups(sc0));
-    // (a wave whose positions are all past c_end keeps m = -inf, l = 0)
-    const float al0 = n0 == -INFINITY ? 1.f : ex2(m0 - n0);
-    const float e0 = valid ? ex2(sc0 - n0) : 0.f;
-    l0 = l0 * al0 + sum_over_8_groups(e0);
-    m0 = n0;
-    a00 *= al0; a01 *= al0;
+    // (m0 = -inf: any valid score raises it; invalid scores never do)
+    if (__builtin_amdgcn_ballot_w64(sc0 > m0 + LAZY_LOG2) != 0) {
+      const float n0 = fmaxf(m0, max_over_8_groups(sc0));
+      const float al0 = m0 == -INFINITY ? 0.f : ex2(m0 - n0);
+      ls *= al0; a00 *= al0; a01 *= al0;
+      m0 = n0;
+    }
+    // (a wave whose positions are all past c_end keeps m = -inf, sums 0)
+    const float e0 = valid ? ex2(sc0 - m0) : 0.f;
+    ls += part == 0 ? e0 : 0.f;
 #pragma unroll
     for (int q = 0; q < 8; q++) {
       const float w0 = lane_value(e0, 8 * q);
@@ -1189,6 +1206,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     slot += SLOT_BYTES;
     if (slot == ring_end) slot = ring;
   }
+  float l0 = wave_sum(ls);
   // the token's own position (wave 3: it has the fewest cached positions in the last chunk)
   if (wave == PK_CW - 1 && p_begin <= pos && pos < p_end) {
     const uint32_t kw = reinterpret_cast<const uint32_t*>(kb)[lane];
