@@ -122,7 +122,7 @@ def cpu_baseline(sample_steps: int = 3):
                       f"model, torch CPU fp32-accumulate restatement (oracle/qwen3_oracle.py)"}
 
 
-PERSISTENT_KERNELS = {"lds_dma": "k_persistent2", "v1": "k_persistent", "v3": "k_persistent3",
+PERSISTENT_KERNELS = {"lds_dma": "k_persistent2", "v1": "k_persistent",
                       "tagged": "k_persistent4"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_c3.txt")
 

@@ -16,7 +16,6 @@
 #include <string>
 #include <vector>
 
-#include "mkd_pk3.h"
 #include "mkd_pk4.h"
 
 using namespace mkd;
@@ -166,7 +165,7 @@ int launch_persistent_b(const MkdStepDesc& d, const MkdSchedule& s, hipStream_t 
     }
     hipLaunchKernelGGL(k_persistent4<B>, dim3(s.grid), dim3(PK_THREADS), PkCfg<B>::LDS_BYTES, st, d, s);
   } else if (d.flags & MKD_FLAG_PK_V3) {
-    hipLaunchKernelGGL(k_persistent3<B>, dim3(s.grid), dim3(P3_THREADS), 0, st, d, s);
+    return fail(MKD_E_INVALID, "the register-streaming persistent variant was removed");
   } else {
     static bool attr_set = false;  // per instantiation; set before the first launch
     if (!attr_set) {

@@ -30,7 +30,7 @@ FLAG_ZERO_FANIN = 2
 FLAG_PK_V1 = 4
 FLAG_PK_V3 = 8
 FLAG_PK_TAGGED = 16
-PERSISTENT_VARIANTS = {"lds_dma": 0, "v1": FLAG_PK_V1, "v3": FLAG_PK_V3, "tagged": FLAG_PK_TAGGED}
+PERSISTENT_VARIANTS = {"lds_dma": 0, "v1": FLAG_PK_V1, "tagged": FLAG_PK_TAGGED}
 
 OP_NOP, OP_QKV, OP_ATTN, OP_OPROJ, OP_GATEUP, OP_DOWN, OP_LMHEAD = range(7)
 OP_NAMES = {OP_NOP: "NOP", OP_QKV: "QKV", OP_ATTN: "ATTN", OP_OPROJ: "OPROJ",

@@ -87,7 +87,7 @@ enum MkdInstWord {
 #define MKD_FLAG_ADVANCE 1u   /* after the step: input_ids[b] = token, cache_seqlens[b] += 1 */
 #define MKD_FLAG_ZERO_FANIN 2u /* set by the persistent launch: last LM task clears fan-in counters */
 #define MKD_FLAG_PK_V1 4u      /* persistent launch, first variant: no weight prefetch (A/B reference) */
-#define MKD_FLAG_PK_V3 8u      /* persistent launch, register-streaming variant (experimental) */
+#define MKD_FLAG_PK_V3 8u      /* reserved: a removed register-streaming variant (launches with it fail) */
 #define MKD_FLAG_PK_TAGGED 16u /* persistent launch, tagged activation exchange (no counters) */
 
 typedef struct MkdStepDesc {
