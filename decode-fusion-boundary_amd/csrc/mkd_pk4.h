@@ -131,12 +131,17 @@ __device__ __forceinline__ uint32_t tw_tag(uint64_t w) { return (uint32_t)(w >> 
 // value its add returns names the barrier generation.)
 struct SyncLds {
   uint32_t* ctr;
+  mutable uint32_t gen;  // barriers this wave has entered (every compute wave runs the same sequence)
   __device__ __forceinline__ void operator()() const {
+#ifdef MKD_PROBE_NO_SYNC  // measurement builds only (no-wait probes): the barrier costs nothing
+    return;
+#endif
     asm volatile("" ::: "memory");
-    uint32_t old = 0;
-    if ((threadIdx.x & 63) == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
-    const uint32_t target = (old / PK_CW + 1) * PK_CW;
+    // the add needs no returned value: barrier k is complete when the counter
+    // (4 adds per barrier) reaches 4 k, and the wave's own add, issued before
+    // its first read, is seen by it (LDS operations of a wave execute in order)
+    const uint32_t target = ++gen * PK_CW;
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(0);
     asm volatile("" ::: "memory");
   }
@@ -192,8 +197,14 @@ __device__ __forceinline__ void p4_trace_poll(const P4& c) {
 // a[] then waits only for loads issued before it.
 template <int N, class Addr>
 __device__ __forceinline__ void poll_issue(Addr addr, uint64_t (&a)[N]) {
+#ifdef MKD_PROBE_SKIP_POLL  // measurement builds only: no dependency waits at all (results are garbage)
+  (void)addr;
+#pragma unroll
+  for (int k = 0; k < N; k++) a[k] = 0;
+#else
 #pragma unroll
   for (int k = 0; k < N; k++) a[k] = ld_co(addr(k));
+#endif
 }
 // Check the first round and keep polling until every word carries `tag`
 // (one round in flight: measured no slower than two, with half the traffic;
@@ -202,6 +213,12 @@ template <int N, class Addr>
 __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_t (&v)[N], uint32_t tag,
                                             const Ws& ws) {
   static_assert(N <= 32, "pending mask");
+#ifdef MKD_PROBE_SKIP_POLL
+  (void)addr; (void)tag; (void)ws;
+#pragma unroll
+  for (int k = 0; k < N; k++) v[k] = a[k];
+  return true;
+#endif
   uint32_t pending = N == 32 ? ~0u : ((1u << N) - 1u);
   // The device error word and the clock are read only by a poll that has
   // already spun 62 rounds: the error word is loaded ahead of a round's polls
@@ -1601,7 +1618,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
               reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(__builtin_amdgcn_kernarg_segment_ptr())));
     return;
   }
-  P4 c{ws, p4_xcc_id() % TW_NREP, (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch)}, flags,
+  P4 c{ws, p4_xcc_id() % TW_NREP, (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch), 0u}, flags,
              reinterpret_cast<float*>(scratch + P4_SCR_RED), reinterpret_cast<float*>(scratch + P4_SCR_RES), xs,
              scratch + P4_SCR_ATTN, reinterpret_cast<uint32_t*>(scratch + P4_SCR_STAGE), 0, nullptr, 0,
              reinterpret_cast<float*>(scratch + p4_scr_part<B>())};
