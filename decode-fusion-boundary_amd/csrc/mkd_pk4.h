@@ -336,7 +336,12 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
   };
   uint64_t first[4 * G];
   if (!from_embed) poll_issue<4 * G>(addr(0), first);    // before any other load of this task
+#ifdef MKD_PROBE_NO_NW  // measurement builds only: constant norm weights (no load)
+  const uint2 wv = make_uint2(0x3f803f80u, 0x3f803f80u);
+  (void)nw;
+#else
   const uint2 wv = ldg2u(nw + k0);
+#endif
   if (from_embed) {
     // first[] was not loaded on this path; consuming it here keeps the compiler
     // from treating those loads as pending afterwards (it would then wait for
@@ -1118,7 +1123,11 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   uint32_t wnw = 0;
   float c0 = 0.f, c1 = 0.f, s0 = 0.f, s1 = 0.f;
   if (wave < 2) {
+#ifdef MKD_PROBE_NO_NW
+    wnw = 0x3f803f80u;
+#else
     wnw = ldg(reinterpret_cast<const uint32_t*>(p4_wptr(d, layer, wave == 0 ? MKD_W_Q_NORM : MKD_W_K_NORM)) + lane);
+#endif
     const int j = (2 * lane) & 63;
     const float* cs = d.rope_cos + (size_t)pos * (HD / 2);
     const float* sn = d.rope_sin + (size_t)pos * (HD / 2);
