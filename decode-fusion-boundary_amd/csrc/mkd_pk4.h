@@ -312,42 +312,43 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
   return p4_agree(c, ok);
 }
 
+// This thread's 4 features of the residual stream, bf16, per row (words
+// pack(f0, f1), pack(f2, f3)): what its last RMSNorm prologue computed. Every
+// workgroup computes the whole residual in each RMSNorm prologue, so the next
+// one needs only the new hidden rows; the published residual words are polled
+// only by the first RMSNorm task of a launch (valid still false).
+template <int B>
+struct ResKeep {
+  uint32_t w[B][2];
+  bool valid;
+};
+
 // Residual add + RMSNorm of B rows into xs (rounding as stage_norm in mkd_tasks.h).
 // from_embed: the rows are the embedding rows of input_ids (layer 0).
-// Otherwise s = hidden + residual from two tagged [MAXB][H/2] buffers.
+// Otherwise s = hidden + residual: the hidden rows from a tagged [MAXB][H/2]
+// buffer, the residual from rk (or, first in a launch, from a tagged buffer).
 // Threads res_first .. res_first + res_n - 1 stage their 4 features of bf16(s),
 // the next residual, published at the end of the task (p4_residual_word).
 template <int B>
 __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c, bool from_embed, size_t hid,
                                               size_t resid, uint32_t tag_in, const uint16_t* nw, int res_first,
-                                              int res_n) {
+                                              int res_n, ResKeep<B>& rk) {
   const int t = p4_tid(), wave = t >> 6, lane = t & 63;
   const int k0 = t * 4;  // features k0..k0+3 = words 2t, 2t+1 of each row
   const bool res_owner = res_first <= t && t < res_first + res_n;
   float s[B][4];
   bool ok = true;
-  // rows in groups of G (two rows at a time keeps the in-flight poll registers small)
-  constexpr int G = B < 2 ? B : 2;
-  auto addr = [&](int b0) {
-    return [=](int k) {
-      return c.ws.tw(((k & 2) ? resid : hid) + (size_t)c.rep * TW_GROUP + (size_t)(b0 + (k >> 2)) * (H / 2) + 2 * t +
-                     (k & 1));
-    };
-  };
-  uint64_t first[4 * G];
-  if (!from_embed) poll_issue<4 * G>(addr(0), first);    // before any other load of this task
+  auto load_nw = [&]() {
 #ifdef MKD_PROBE_NO_NW  // measurement builds only: constant norm weights (no load)
-  const uint2 wv = make_uint2(0x3f803f80u, 0x3f803f80u);
-  (void)nw;
+    (void)nw;
+    return make_uint2(0x3f803f80u, 0x3f803f80u);
 #else
-  const uint2 wv = ldg2u(nw + k0);
+    return ldg2u(nw + k0);
 #endif
+  };
+  uint2 wv;
   if (from_embed) {
-    // first[] was not loaded on this path; consuming it here keeps the compiler
-    // from treating those loads as pending afterwards (it would then wait for
-    // every memory operation before it next writes their registers)
-#pragma unroll
-    for (int k = 0; k < 4 * G; k++) asm volatile("" ::"v"((uint32_t)first[k]));
+    wv = load_nw();
 #pragma unroll
     for (int b = 0; b < B; b++) {
       int64_t id = b < d.rows ? d.input_ids[b] : 0;
@@ -358,7 +359,45 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
       const uint2 e = *reinterpret_cast<const uint2*>(d.embed + (size_t)id * H + k0);
       s[b][0] = bf_lo(e.x); s[b][1] = bf_hi(e.x); s[b][2] = bf_lo(e.y); s[b][3] = bf_hi(e.y);
     }
+  } else if (rk.valid) {
+    // hidden words only: rows in groups of GH (2 words each)
+    constexpr int GH = B < 4 ? B : 4;
+    auto haddr = [&](int b0) {
+      return [=](int k) { return c.ws.tw(hid + (size_t)c.rep * TW_GROUP + (size_t)(b0 + (k >> 1)) * (H / 2) + 2 * t + (k & 1)); };
+    };
+    uint64_t first[2 * GH];
+    poll_issue<2 * GH>(haddr(0), first);  // before any other load of this task
+    wv = load_nw();
+#pragma unroll
+    for (int b0 = 0; b0 < B; b0 += GH) {
+      uint64_t v[2 * GH];
+      if (b0 == 0) {
+        ok = poll_finish<2 * GH>(haddr(0), first, v, tag_in, c.ws);
+        p4_trace_poll(c);
+      } else {
+        ok = ok && poll_tagged<2 * GH>(haddr(b0), v, tag_in, c.ws);
+      }
+#pragma unroll
+      for (int g = 0; g < GH; g++) {
+        const int b = b0 + g;
+        const uint32_t h0 = (uint32_t)v[2 * g], h1 = (uint32_t)v[2 * g + 1];
+        const uint32_t r0 = rk.w[b][0], r1 = rk.w[b][1];
+        s[b][0] = bf_lo(h0) + bf_lo(r0); s[b][1] = bf_hi(h0) + bf_hi(r0);
+        s[b][2] = bf_lo(h1) + bf_lo(r1); s[b][3] = bf_hi(h1) + bf_hi(r1);
+      }
+    }
   } else {
+    // rows in groups of G (two rows at a time keeps the in-flight poll registers small)
+    constexpr int G = B < 2 ? B : 2;
+    auto addr = [&](int b0) {
+      return [=](int k) {
+        return c.ws.tw(((k & 2) ? resid : hid) + (size_t)c.rep * TW_GROUP + (size_t)(b0 + (k >> 2)) * (H / 2) + 2 * t +
+                       (k & 1));
+      };
+    };
+    uint64_t first[4 * G];
+    poll_issue<4 * G>(addr(0), first);  // before any other load of this task
+    wv = load_nw();
 #pragma unroll
     for (int b0 = 0; b0 < B; b0 += G) {
       uint64_t v[4 * G];
@@ -378,6 +417,13 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
       }
     }
   }
+  // the new residual, for the next RMSNorm prologue of this launch
+#pragma unroll
+  for (int b = 0; b < B; b++) {
+    rk.w[b][0] = pack_bf2(s[b][0], s[b][1]);
+    rk.w[b][1] = pack_bf2(s[b][2], s[b][3]);
+  }
+  rk.valid = true;
   const float w4[4] = {bf_lo(wv.x), bf_hi(wv.x), bf_lo(wv.y), bf_hi(wv.y)};
   // consumed here, before the abort return below: a load left unconsumed on
   // that path would make the compiler wait for all memory operations at the
@@ -389,8 +435,8 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
     uint32_t* stage = c.stage + c.par * P4_STAGE_WORDS;
 #pragma unroll
     for (int b = 0; b < B; b++) {
-      stage[((t - res_first) * B + b) * 2] = pack_bf2(s[b][0], s[b][1]);
-      stage[((t - res_first) * B + b) * 2 + 1] = pack_bf2(s[b][2], s[b][3]);
+      stage[((t - res_first) * B + b) * 2] = rk.w[b][0];
+      stage[((t - res_first) * B + b) * 2 + 1] = rk.w[b][1];
     }
   }
 #pragma unroll
@@ -649,7 +695,7 @@ __device__ __forceinline__ ResRange p4_res_range(const Inst& w) {
 }
 
 template <int B>
-__device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, const Inst& w) {
+__device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, const Inst& w, ResKeep<B>& rk) {
   const int layer = w.layer;
   const uint32_t tag = p4_tag(c.epoch, layer);
   const int t = p4_tid();
@@ -657,17 +703,17 @@ __device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, c
     case MKD_OP_QKV: {
       const ResRange r = p4_res_range<QKV_N / 256>(w);
       const uint16_t* nw = p4_wptr(d, layer, MKD_W_LN_IN);
-      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, r.first, r.n);
-      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, r.first, r.n);
+      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, r.first, r.n, rk);
+      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, r.first, r.n, rk);
     }
     case MKD_OP_GATEUP: {
       const ResRange r = p4_res_range<I / 256>(w);
-      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST), r.first, r.n);
+      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST), r.first, r.n, rk);
     }
     case MKD_OP_OPROJ: return p4_stage_copy<B, QS>(c, TW_ATTN, tag);
     case MKD_OP_DOWN: return p4_stage_copy<B, I>(c, TW_ACT, tag);
     case MKD_OP_LMHEAD:
-      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, d.num_layers - 1), d.final_norm, 0, 0);
+      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, d.num_layers - 1), d.final_norm, 0, 0, rk);
     default: return true;
   }
 }
@@ -1633,6 +1679,8 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
              reinterpret_cast<float*>(scratch + p4_scr_part<B>())};
   bool aborted = false;
   int cc = 0;
+  ResKeep<B> rk;  // residual stream of this thread's features (after a first RMSNorm task)
+  rk.valid = false;
   cint32_t* crow = as_const(row);
   Inst w_next = n_inst > 0 ? load_inst(crow) : Inst{};
   for (int i = 0; i < n_inst; i++) {
@@ -1665,7 +1713,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
       if (threadIdx.x == 0) st_co(ws.line(CTR_ERR), ERR_BAD_INST);
       aborted = true;
     }
-    if (!aborted) aborted = !p4_prologue<B>(d, c, w);
+    if (!aborted) aborted = !p4_prologue<B>(d, c, w, rk);
     if (tr != nullptr && threadIdx.x == 0) tr[1] = wall_clock64();
     LmArg<B> best;
     best.reset();

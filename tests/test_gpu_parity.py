@@ -169,6 +169,39 @@ def test_full_depth_random_kv_context_256(batch, variant):
 
 
 @pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("batch", [1, 4])
+def test_layer_segments_match_one_launch(batch, variant):
+    """fusion_groups = 4 (four persistent launches of two layers each) gives
+    bit-identical logits to one launch: values cross a launch boundary only
+    through the workspace (the tagged kernel's residual, kept in registers
+    within a launch, is read back from its published words), and both agree
+    with the oracle."""
+    print(f"case: 8 layers as 4 launches vs 1, batch={batch} variant={variant}", flush=True)
+    ids = [(1231 * (b + 1)) % 151936 for b in range(batch)]
+    pos = [200 - 7 * b for b in range(batch)]
+    tables = [[b] for b in range(batch)]
+    out = []
+    for groups in (1, 4):
+        h = Harness(num_layers=8, num_blocks=batch + 1, kv_fill_seed=5, fusion_groups=groups, variant=variant)
+        if groups == 1:
+            kv_before = h.kv_cpu.clone()
+        toks, logits = h.step(ids, pos, tables)
+        if groups == 1:
+            ref_toks, ref_logits = h.oracle_step(ids, pos, tables)
+        out.append((toks, logits))
+        h.close()
+    (t1, l1), (t4, l4) = out
+    torch_logits = _torch_path_logits(8, kv_before, ids, pos, tables)
+    err = max_abs(l1, ref_logits)
+    bound = LOGIT_TOL + 1.5 * max_abs(torch_logits, ref_logits)
+    print(f"  tokens {t1} / {t4} oracle {ref_toks}; max|dlogit| one launch vs oracle {err:.3e} (bound "
+          f"{bound:.3e}), one vs four launches {max_abs(l1, l4):.3e}", flush=True)
+    assert t1 == t4 and torch.equal(l1, l4)
+    assert err <= bound
+    check_tokens(t1, ref_toks, ref_logits, bound)
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
 def test_inactive_row_leaves_its_pages_untouched(variant):
     """row_active=0 skips only the KV write (reference row_contract.py:1-52)."""
     print(f"case: inactive row, variant={variant}", flush=True)
