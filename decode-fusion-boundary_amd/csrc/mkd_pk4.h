@@ -317,6 +317,10 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
 // workgroup computes the whole residual in each RMSNorm prologue, so the next
 // one needs only the new hidden rows; the published residual words are polled
 // only by the first RMSNorm task of a launch (valid still false).
+// Gate/up task word a2 flag (tagged kernel): publish the residual, read by
+// the next layer's QKV prologue in the next launch (the last layer of a layer
+// segment that is not the step's last).
+constexpr int GATEUP_PUBLISH_RES = 1;
 template <int B>
 struct ResKeep {
   uint32_t w[B][2];
@@ -700,15 +704,17 @@ __device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, c
   const uint32_t tag = p4_tag(c.epoch, layer);
   const int t = p4_tid();
   switch (w.op) {
+    // (the residual after QKV is consumed by the gate/up prologue of the same
+    // layer, always in the same launch: never published)
     case MKD_OP_QKV: {
-      const ResRange r = p4_res_range<QKV_N / 256>(w);
       const uint16_t* nw = p4_wptr(d, layer, MKD_W_LN_IN);
-      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, r.first, r.n, rk);
-      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, r.first, r.n, rk);
+      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, 0, 0, rk);
+      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, 0, 0, rk);
     }
     case MKD_OP_GATEUP: {
       const ResRange r = p4_res_range<I / 256>(w);
-      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST), r.first, r.n, rk);
+      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST), r.first,
+                              (w.a2 & GATEUP_PUBLISH_RES) ? r.n : 0, rk);
     }
     case MKD_OP_OPROJ: return p4_stage_copy<B, QS>(c, TW_ATTN, tag);
     case MKD_OP_DOWN: return p4_stage_copy<B, I>(c, TW_ACT, tag);
@@ -918,8 +924,7 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
   const int n = (w.a1 >> 1) << (LB + LR);  // (channel or row) pairs x rows x replicas
   uint8_t* const twb = reinterpret_cast<uint8_t*>(c.ws.tw(BASE + (uint32_t)(w.a0 >> 1)));
   ResWord rw{nullptr, 0};
-  if (OP == MKD_OP_QKV) rw = p4_residual_word<B, QKV_N / 256>(c, w, TW_RES1, tag);
-  if (OP == MKD_OP_GATEUP) rw = p4_residual_word<B, I / 256>(c, w, TW_RES2, tag);
+  if (OP == MKD_OP_GATEUP && (w.a2 & GATEUP_PUBLISH_RES)) rw = p4_residual_word<B, I / 256>(c, w, TW_RES2, tag);
   for (int e = fo; e < n; e += PK_CW * 64) {
     const int r = e & ((1 << LR) - 1), b = (e >> LR) & (B - 1), i = e >> (LR + LB);
     float v0, v1;

@@ -24,6 +24,8 @@ KV_CHUNK = 32            # positions per KV chunk the tagged kernel stages (bloc
 # ATTN_ONE_HEAD set, and ATTN_QHEAD set for the second head (2h + 1) of KV head h
 ATTN_QHEAD = 64
 ATTN_ONE_HEAD = 128
+# GATEUP task word a2 (tagged kernel): publish the residual for the next launch
+GATEUP_PUBLISH_RES = 1
 
 FLAG_ADVANCE = 1
 FLAG_ZERO_FANIN = 2

@@ -26,10 +26,11 @@ k = 0..7 the QKV blocks of KV head k, 8 attention, 9 O-proj, 10 gate/up,
 
 from __future__ import annotations
 
+import dataclasses
 from dataclasses import dataclass, field
 
 from .native import (
-    ATTN_ONE_HEAD, ATTN_QHEAD, INST_WORDS, MAX_BATCH, MAX_LM_SLOTS, MAX_SPLITS, OP_ATTN, OP_DOWN, OP_GATEUP,
+    ATTN_ONE_HEAD, ATTN_QHEAD, GATEUP_PUBLISH_RES, INST_WORDS, MAX_BATCH, MAX_LM_SLOTS, MAX_SPLITS, OP_ATTN, OP_DOWN, OP_GATEUP,
     OP_LMHEAD, OP_OPROJ, OP_QKV,
 )
 
@@ -328,6 +329,11 @@ def build_segments(batch: int, attn_splits: int, num_wgs: int, num_layers: int =
     out = []
     for start, end in split_layers(num_layers, groups):
         seg = [s for s in stages if start <= s.layer < end or (end == num_layers and s.op == OP_LMHEAD)]
+        if q_head_tasks and end < num_layers:
+            # the tagged kernel keeps the residual stream in registers within a
+            # launch; the segment's last gate/up tasks publish it for the next one
+            seg = [Stage(s.op, s.layer, [dataclasses.replace(t, a2=t.a2 | GATEUP_PUBLISH_RES) for t in s.tasks])
+                   if s.op == OP_GATEUP and s.layer == end - 1 else s for s in seg]
         out.append(Schedule(batch=batch, attn_splits=attn_splits, num_layers=num_layers,
                             grid=num_wgs, stages=seg, rows=place_xcd_aware(seg, num_wgs)))
     return out

@@ -111,6 +111,22 @@ def test_tagged_exchange_preconditions_at_256_cus(batch, splits):
         _check_tagged_preconditions(build_segments(batch, splits, 256, 28, 1))
 
 
+def test_gate_up_publishes_residual_only_at_segment_ends():
+    """Tagged schedule: the gate/up tasks of the last layer of each segment but
+    the step's last carry the publish flag; no other task does."""
+    for groups in (1, 4, 28):
+        segs = build_segments(2, 1, 256, 28, groups, q_head_tasks=True)
+        ends = {seg.stages[-2].layer if seg.stages[-1].op == native.OP_LMHEAD else seg.stages[-1].layer for seg in segs}
+        for seg in segs:
+            for row in seg.rows:
+                for t in row:
+                    flagged = t.op == native.OP_GATEUP and bool(t.a2 & native.GATEUP_PUBLISH_RES)
+                    assert flagged == (t.op == native.OP_GATEUP and t.layer in ends and t.layer < 27)
+    # the counter-protocol schedule is unchanged
+    for seg in build_segments(2, 1, 256, 28, 4):
+        assert all(t.a2 == 0 for row in seg.rows for t in row if t.op == native.OP_GATEUP)
+
+
 def test_query_head_attention_tasks():
     """The tagged schedule has two ATTN tasks per (row, KV head, split): query
     heads 2h and 2h + 1, flagged in a0 and placed on the KV head's die."""
