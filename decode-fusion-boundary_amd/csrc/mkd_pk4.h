@@ -290,7 +290,9 @@ constexpr int largest_divisor_le8(int n) {
 template <int B, int K>
 __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t tag) {
   constexpr int PER = B * (K / 2) / 256;  // words per thread
-  constexpr int NB = largest_divisor_le8(PER);
+  // (batch 8, down: 12-word groups, four rounds instead of six)
+  constexpr int NB = B >= 8 && K == 3072 ? 12 : largest_divisor_le8(PER);
+  static_assert(PER % NB == 0, "whole groups");
   const int t = p4_tid();
   const uint64_t* src = c.ws.tw(base + (size_t)c.rep * TW_GROUP);
   uint32_t* dst = reinterpret_cast<uint32_t*>(c.xs);
