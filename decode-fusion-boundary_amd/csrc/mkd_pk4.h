@@ -1145,6 +1145,45 @@ __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x)
 // The four waves are merged at the end; the token's own K/V (not yet in the
 // cache when this task reads it) comes from LDS. The last split folds in the
 // other splits' tagged partials. nch returns the task's KV chunk count.
+// Last split of an attention task: wave w folds the partials (num, max, sum:
+// the same unnormalized base-2 form as its own accumulators, for this lane's
+// dims 2 lane, 2 lane + 1) of splits w, w + 4, w + 8, w + 12 into its own, SPR
+// splits per poll round.
+__device__ __forceinline__ void p4_fold_splits(const Ws ws, size_t pbase, int nsplit, int g, uint32_t tag, float& m0,
+                                               float& l0, float& a00, float& a01, bool& ok) {
+  const int wave = p4_tid() >> 6, lane = threadIdx.x & 63;
+  constexpr int SPW = (MAXS - 1 + PK_CW - 1) / PK_CW;  // splits per wave
+#ifndef MKD_FOLD_SPR
+#define MKD_FOLD_SPR 2
+#endif
+  constexpr int SPR = MKD_FOLD_SPR;                     // splits per poll round
+#pragma unroll
+  for (int q0 = 0; q0 < SPW; q0 += SPR) {
+    if (wave + PK_CW * q0 >= nsplit - 1) break;
+    uint64_t e[4 * SPR];
+    // (entries past the last split repeat its words)
+    const bool okp = poll_tagged<4 * SPR>(
+        [&](int k) {
+          const int sp = min(wave + PK_CW * (q0 + (k >> 2)), nsplit - 2), f = k & 3;
+          const size_t ps = pbase + (size_t)sp * PART_STRIDE;
+          return ws.tw(ps + (f < 2 ? (size_t)(g * HD + 2 * lane + f) : (size_t)(GROUP * HD + (f - 2) * GROUP + g)));
+        },
+        e, tag, ws);
+    ok = ok && okp;
+#pragma unroll
+    for (int q = 0; q < SPR; q++) {
+      if (wave + PK_CW * (q0 + q) >= nsplit - 1) break;
+      const float ms = __uint_as_float((uint32_t)e[4 * q + 2]);
+      if (ms == -INFINITY) continue;  // an empty split
+      const float nm = fmaxf(m0, ms);
+      const float sa = m0 == -INFINITY ? 0.f : ex2(m0 - nm), sb = ex2(ms - nm);
+      a00 = a00 * sa + __uint_as_float((uint32_t)e[4 * q]) * sb;
+      a01 = a01 * sa + __uint_as_float((uint32_t)e[4 * q + 1]) * sb;
+      l0 = l0 * sa + __uint_as_float((uint32_t)e[4 * q + 3]) * sb;
+      m0 = nm;
+    }
+  }
+}
 constexpr int ATTN_QHEAD = 64, ATTN_ONE_HEAD = 128;  // task word a0 flags (b * 8 + h < 64)
 template <int B, int NS>
 __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int a0, int split, int nsplit,
@@ -1297,6 +1336,17 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     const uint32_t vw = reinterpret_cast<const uint32_t*>(vb)[lane];
     a00 = a00 * al0 + e0 * bf_lo(vw); a01 = a01 * al0 + e0 * bf_hi(vw);
   }
+  const size_t pbase = TW_APART + (((size_t)b * NKV + h) * MAXS) * PART_STRIDE;  // split partials of (b, h)
+  // (batch 2 and 4: inlined at batch 1 and 8, where it never helps a short
+  // context, this code slowed the short-context step: 8-15 us, measured)
+  constexpr bool FOLD = B == 2 || B == 4;
+  if constexpr (FOLD) {
+    if (nsplit > 1 && split == nsplit - 1) {
+      // last split: wave w folds the other splits' partials into its own
+      // accumulators (p4_fold_splits); the waves' merge below then combines them
+      p4_fold_splits(c.ws, pbase, nsplit, g, tag, m0, l0, a00, a01, ok);
+    }
+  }
   // merge the waves in LDS
   reinterpret_cast<float2*>(mrg + wave * HD)[lane] = make_float2(a00, a01);
   if (lane == 0) { mrg_ml[wave] = m0; mrg_ml[PK_CW + wave] = l0; }
@@ -1315,23 +1365,23 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
       den += mrg_ml[PK_CW + ww] * sc;
     }
   }
-  if (nsplit > 1) {
-    const size_t pbase = TW_APART + (((size_t)b * NKV + h) * MAXS) * PART_STRIDE;
-    if (split != nsplit - 1) {
-      // read only by the last split of this (row, query head)
-      uint64_t* part = c.ws.tw(pbase + (size_t)split * PART_STRIDE);
-      if (half == 0) {
-        st_tw(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
-        if (dd == 0) {
-          st_tw(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
-          st_tw(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
-        }
+  if (nsplit > 1 && split != nsplit - 1) {
+    // read only by the last split of this (row, query head)
+    uint64_t* part = c.ws.tw(pbase + (size_t)split * PART_STRIDE);
+    if (half == 0) {
+      st_tw(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
+      if (dd == 0) {
+        st_tw(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
+        st_tw(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
       }
-      c.sync();  // the scratch is reused by this workgroup's next task
-      return true;
     }
-    // last split: fold in the other splits' partials (online, -inf = empty split)
-    for (int sp = 0; sp < nsplit - 1; sp++) {
+    c.sync();  // the scratch is reused by this workgroup's next task
+    return true;
+  }
+  if constexpr (!FOLD) {
+    // batch 1 and 8: the last split folds the other splits' partials here,
+    // one split per round
+    for (int sp = 0; nsplit > 1 && sp < nsplit - 1; sp++) {
       const size_t ps = pbase + (size_t)sp * PART_STRIDE;
       uint64_t e[3];
       ok = ok && poll_tagged<3>(
