@@ -247,10 +247,7 @@ __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_
         return false;
       }
     }
-#ifndef MKD_POLL_SLEEP
-#define MKD_POLL_SLEEP 1
-#endif
-    __builtin_amdgcn_s_sleep(MKD_POLL_SLEEP);
+    __builtin_amdgcn_s_sleep(1);  // (longer pauses measured slower at every batch size)
     if ((spin & 63u) == 62u) err = ld_co(ws.line(CTR_ERR));
 #pragma unroll
     for (int k = 0; k < N; k++)
@@ -1153,10 +1150,7 @@ __device__ __forceinline__ void p4_fold_splits(const Ws ws, size_t pbase, int ns
                                                float& l0, float& a00, float& a01, bool& ok) {
   const int wave = p4_tid() >> 6, lane = threadIdx.x & 63;
   constexpr int SPW = (MAXS - 1 + PK_CW - 1) / PK_CW;  // splits per wave
-#ifndef MKD_FOLD_SPR
-#define MKD_FOLD_SPR 2
-#endif
-  constexpr int SPR = MKD_FOLD_SPR;                     // splits per poll round
+  constexpr int SPR = 2;                                // splits per poll round
 #pragma unroll
   for (int q0 = 0; q0 < SPW; q0 += SPR) {
     if (wave + PK_CW * q0 >= nsplit - 1) break;
@@ -1693,11 +1687,7 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
     }
 #endif
     raw_barrier();
-#ifdef MKD_EXP_LOOKAHEAD
-    while (cur.nch > 0 && issued < g * G + min(Cfg::NS, MKD_EXP_LOOKAHEAD)) issue_one();
-#else
     while (cur.nch > 0 && issued < g * G + Cfg::NS) issue_one();
-#endif
   }
 }
 
