@@ -1372,9 +1372,11 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     c.sync();  // the scratch is reused by this workgroup's next task
     return true;
   }
-  if constexpr (!FOLD) {
-    // batch 1 and 8: the last split folds the other splits' partials here,
-    // one split per round
+  if constexpr (B == 1) {
+    // batch 1: the last split folds the other splits' partials here, one split
+    // per round (both thread halves alike: dividing the splits between them,
+    // like batch 8, measured 4 % faster at ctx 1500 but slowed the
+    // short-context step by 1 %)
     for (int sp = 0; nsplit > 1 && sp < nsplit - 1; sp++) {
       const size_t ps = pbase + (size_t)sp * PART_STRIDE;
       uint64_t e[3];
@@ -1391,6 +1393,55 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
       num = num * sa + ns * sb;
       den = den * sa + ls * sb;
       M = nm;
+    }
+  }
+  if constexpr (B == 8) {
+    // batch 8: the last split folds the other splits' partials here, one
+    // split per round; the two thread halves (the same dims) take the even and
+    // the odd splits, then combine (even, odd) in that order
+    if (nsplit > 1) {
+      float Mh = half == 0 ? M : -INFINITY, nh = half == 0 ? num : 0.f, dh = half == 0 ? den : 0.f;
+      for (int sp = half; sp < nsplit - 1; sp += 2) {
+        const size_t ps = pbase + (size_t)sp * PART_STRIDE;
+        uint64_t e[3];
+        ok = ok && poll_tagged<3>(
+                       [&](int k) {
+                         return c.ws.tw(ps + (k == 0 ? (size_t)(g * HD + dd) : (size_t)(GROUP * HD + (k - 1) * GROUP + g)));
+                       },
+                       e, tag, c.ws);
+        const float ns = __uint_as_float((uint32_t)e[0]), ms = __uint_as_float((uint32_t)e[1]);
+        const float ls = __uint_as_float((uint32_t)e[2]);
+        if (ms == -INFINITY) continue;
+        const float nm = fmaxf(Mh, ms);
+        const float sa = Mh == -INFINITY ? 0.f : ex2(Mh - nm), sb = ex2(ms - nm);
+        nh = nh * sa + ns * sb;
+        dh = dh * sa + ls * sb;
+        Mh = nm;
+      }
+      // through the q/k/v scratch (free after the waves' merge): the odd half's
+      // fold, then the combined result
+      float* xf = reinterpret_cast<float*>(smem);  // [128] num, then max, sum (odd half), max, sum (combined)
+      if (half == 1) {
+        xf[dd] = nh;
+        if (dd == 0) { xf[HD] = Mh; xf[HD + 1] = dh; }
+      }
+      c.sync();
+      if (half == 0) {
+        const float mo = xf[HD], no = xf[dd], lo = xf[HD + 1];
+        if (mo != -INFINITY) {
+          const float nm = fmaxf(Mh, mo);
+          const float sa = Mh == -INFINITY ? 0.f : ex2(Mh - nm), sb = ex2(mo - nm);
+          nh = nh * sa + no * sb;
+          dh = dh * sa + lo * sb;
+          Mh = nm;
+        }
+      }
+      if (half == 0) {
+        xf[dd] = nh;  // (this thread's own entry, read above)
+        if (dd == 0) { xf[HD + 2] = Mh; xf[HD + 3] = dh; }
+      }
+      c.sync();
+      num = xf[dd]; M = xf[HD + 2]; den = xf[HD + 3];
     }
   }
   const uint32_t mine = f2bf(num / den);
