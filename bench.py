@@ -44,7 +44,7 @@ def step_bytes(contexts: list[int]) -> int:
     return WEIGHT_BYTES + sum(KV_BYTES_PER_POS * c + KV_BYTES_PER_POS + EMBED_ROW_BYTES for c in contexts)
 
 
-def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="tagged"):
+def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="tagged", fusion_groups=1):
     import torch
     from nanovllm.backends.megakernel.taskgraph import TaskGraphDecoder
     from nanovllm.backends.megakernel.weights import weights_from_synthetic
@@ -54,13 +54,33 @@ def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="ta
     w = weights_from_synthetic(synth, device="cuda")
     kv = torch.zeros(2, num_layers, num_blocks, 256, 8, 128, dtype=torch.bfloat16, device="cuda")
     dec = TaskGraphDecoder(w, k_cache=kv[0], v_cache=kv[1], block_size=256, num_cache_blocks=num_blocks,
-                           max_model_len=2048, launch=launch, persistent_variant=variant)
+                           max_model_len=2048, launch=launch, persistent_variant=variant,
+                           fusion_groups=fusion_groups)
     return synth, w, kv, dec
 
 
+def ragged_tables(start_ctx: list[int], steps: int, num_blocks: int, block_size: int = 256, cols: int = 8,
+                  seed: int = 0) -> list[list[int]]:
+    """Block tables drawn from a shuffled page pool (rows own scattered, non-contiguous
+    pages); each row gets the pages its context reaches, the rest of its row is 0."""
+
+    import random
+
+    rng = random.Random(seed)
+    pool = list(range(num_blocks))
+    rng.shuffle(pool)
+    tables = []
+    for c in start_ctx:
+        need = (c + steps + block_size - 1) // block_size  # positions c .. c+steps-1
+        assert need <= cols and len(pool) >= need, "page pool too small for the workload"
+        tables.append([pool.pop() for _ in range(need)] + [0] * (cols - need))
+    return tables
+
+
 def time_decode(dec, batch: int, start_ctx: list[int], steps: int, warmup: int, mode: str, seed: int = 0,
-                per_launch_events: bool = False):
-    """Returns (seconds for `steps` steps, per-launch durations in ms or None, contexts per step)."""
+                per_launch_events: bool = False, tables=None):
+    """Returns (seconds for `steps` steps, per-launch durations in ms or None, contexts per step).
+    `tables` (list of rows) overrides the default contiguous block tables."""
 
     import torch
 
@@ -68,7 +88,9 @@ def time_decode(dec, batch: int, start_ctx: list[int], steps: int, warmup: int, 
     ids = torch.randint(0, VOCAB, (batch,), generator=gen, dtype=torch.int64).cuda()
     pos = torch.tensor(start_ctx, dtype=torch.int64).cuda()
     pages = 8
-    tables = torch.tensor([[b * pages + j for j in range(pages)] for b in range(batch)], dtype=torch.int32).cuda()
+    if tables is None:
+        tables = [[b * pages + j for j in range(pages)] for b in range(batch)]
+    tables = torch.tensor(tables, dtype=torch.int32).cuda()
     max_ctx = max(start_ctx) + max(steps, warmup) + 1
     run = dec.prepare_steps(batch, max_ctx, mode=mode)
     dec.stage_rows(ids, pos, tables)
@@ -156,6 +178,59 @@ def copy_calibration(nbytes: int = 1 << 30, launches: int = 4):
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "launches": launches}))
 
 
+def long_context_runs(workload: str, steps: int, warmup: int) -> dict:
+    """C4 (batch 8, 512-token prompts) or C5 (batch 1/2/4/8, prompt lengths
+    U[1024,1920], ragged block tables): device us/step of the persistent kernel
+    and of the captured per-op hipGraph, same kernels, same inputs. The cache holds
+    the previous run's (or zero) K/V in the prompt positions: the step's work and
+    bytes do not depend on their values."""
+
+    import random
+
+    num_blocks = 8 * 8 + 8
+    _, _, _, dec = build_decoder(num_blocks=num_blocks)
+    rng = random.Random(0)
+    if workload == "c4":
+        cases = [(8, [512] * 8)]
+    else:
+        cases = [(b, [rng.randint(1024, 1920) for _ in range(b)]) for b in (1, 2, 4, 8)]
+    out = {}
+    for b, start in cases:
+        tables = ragged_tables(start, max(steps, warmup), num_blocks, seed=b)
+        for mode in ("persistent", "graph"):
+            _, durs, ctxs = time_decode(dec, b, start, steps, warmup, mode, per_launch_events=True, tables=tables)
+            us = sum(durs) / len(durs) * 1e3
+            nbytes = sum(step_bytes(c) for c in ctxs) / len(ctxs)
+            out[f"{mode}_b{b}"] = {"us_per_step": round(us, 2), "tok_per_s": round(b / us * 1e6, 1),
+                                   "GBps": round(nbytes / us / 1e3, 1),
+                                   "floor_us": round(nbytes / HBM_PEAK_GBPS / 1e3, 2),
+                                   "splits": dec.splits_for(max(start) + steps + 1),
+                                   "ctx": [min(start) + 1, max(start) + steps]}
+    dec.close()
+    return out
+
+
+def fusion_sweep(steps: int, warmup: int) -> dict:
+    """Layer segments per step (fusion_groups g: g persistent launches of 28/g
+    layers each, the LM head in the last) at batch 1 and 8, short context."""
+
+    import torch
+
+    out = {}
+    synth = None
+    for g in (1, 2, 4, 7, 14, 28):
+        _, _, _, dec = build_decoder(num_blocks=72, fusion_groups=g)
+        for b in (1, 8):
+            _, durs, ctxs = time_decode(dec, b, [0] * b, steps, warmup, "persistent", per_launch_events=True)
+            us = sum(durs) / len(durs) * 1e3
+            out[f"g{g}_b{b}"] = {"us_per_step": round(us, 2), "launches_per_step": g,
+                                 "GBps": round(sum(step_bytes(c) for c in ctxs) / len(ctxs) / us / 1e3, 1)}
+        dec.close()
+        del dec
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,6 +245,10 @@ def main():
     ap.add_argument("--only-kernel", action="store_true", help="timed loop only (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 1 GiB device copy only (counter calibration under rocprofv3 --pmc)")
+    ap.add_argument("--workload", default="c3", choices=["c3", "c4", "c5"],
+                    help="c3: the headline line (default); c4/c5: long-context persistent vs hipGraph table")
+    ap.add_argument("--fusion-sweep", action="store_true",
+                    help="persistent kernel at fusion_groups 1/2/4/7/14/28, batch 1 and 8")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode step runs TP=1 on a single MI355X; "
@@ -183,6 +262,17 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.workload != "c3" or args.fusion_sweep:
+        res = {"metric": "device us/decode-step & tok/s at batch 1-8 vs 1.19GB HBM weight floor", "unit": "us/step",
+               "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "bf16",
+               "data": "synthetic (random-init bf16 weights seed 0, random token ids)"}
+        if args.fusion_sweep:
+            res["fusion_sweep"] = fusion_sweep(args.steps, args.warmup)
+        else:
+            res["workload"] = args.workload
+            res["modes"] = long_context_runs(args.workload, args.steps, args.warmup)
+        print(json.dumps(res))
         return
     _, _, _, dec = build_decoder(num_blocks=8 * 8 + 8, variant=args.variant)
     start = [0] * args.batch
