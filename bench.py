@@ -44,7 +44,8 @@ def step_bytes(contexts: list[int]) -> int:
     return WEIGHT_BYTES + sum(KV_BYTES_PER_POS * c + KV_BYTES_PER_POS + EMBED_ROW_BYTES for c in contexts)
 
 
-def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="tagged", fusion_groups=1):
+def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="tagged", fusion_groups=1,
+                  attn_splits=1):
     import torch
     from nanovllm.backends.megakernel.taskgraph import TaskGraphDecoder
     from nanovllm.backends.megakernel.weights import weights_from_synthetic
@@ -55,7 +56,7 @@ def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="ta
     kv = torch.zeros(2, num_layers, num_blocks, 256, 8, 128, dtype=torch.bfloat16, device="cuda")
     dec = TaskGraphDecoder(w, k_cache=kv[0], v_cache=kv[1], block_size=256, num_cache_blocks=num_blocks,
                            max_model_len=2048, launch=launch, persistent_variant=variant,
-                           fusion_groups=fusion_groups)
+                           fusion_groups=fusion_groups, attn_splits=attn_splits)
     return synth, w, kv, dec
 
 
@@ -245,6 +246,9 @@ def main():
     ap.add_argument("--only-kernel", action="store_true", help="timed loop only (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 1 GiB device copy only (counter calibration under rocprofv3 --pmc)")
+    ap.add_argument("--attn-splits", type=int, default=1, help="minimum split-KV factor (megakernel_attn_splits)")
+    ap.add_argument("--start-ctx", type=int, default=0,
+                    help="cached positions per row before the first timed step (c3 path; the KV holds zeros)")
     ap.add_argument("--workload", default="c3", choices=["c3", "c4", "c5"],
                     help="c3: the headline line (default); c4/c5: long-context persistent vs hipGraph table")
     ap.add_argument("--fusion-sweep", action="store_true",
@@ -274,8 +278,8 @@ def main():
             res["modes"] = long_context_runs(args.workload, args.steps, args.warmup)
         print(json.dumps(res))
         return
-    _, _, _, dec = build_decoder(num_blocks=8 * 8 + 8, variant=args.variant)
-    start = [0] * args.batch
+    _, _, _, dec = build_decoder(num_blocks=8 * 8 + 8, variant=args.variant, attn_splits=args.attn_splits)
+    start = [args.start_ctx] * args.batch
     elapsed, durs, contexts = time_decode(dec, args.batch, start, args.steps, args.warmup, args.mode,
                                           per_launch_events=True)
     if args.only_kernel:

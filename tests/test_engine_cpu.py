@@ -95,13 +95,13 @@ def test_config_validation(tmp_path):
     assert cfg.max_model_len == 40960 and cfg.hf_config.num_hidden_layers == 1
 
 
-def test_engine_megakernel_falls_back_with_reason_on_cpu():
+def test_engine_megakernel_falls_back_with_reason_on_cpu(tmp_path):
     """No GPU here: the backend is disabled at startup with an explicit reason,
     and every decode step reports the torch path plus that reason."""
     from nanovllm import LLM, SamplingParams
     from nanovllm.synthetic import write_model_dir
 
-    path = write_model_dir(os.path.join(ROOT, "_work", "test_model_2l"), num_layers=2)
+    path = write_model_dir(str(tmp_path / "model_2l"), num_layers=2)
     with warnings.catch_warnings(record=True) as caught:
         warnings.simplefilter("always")
         llm = LLM(path, max_model_len=2048, num_kvcache_blocks=4, decode_backend="megakernel")
@@ -113,11 +113,11 @@ def test_engine_megakernel_falls_back_with_reason_on_cpu():
     assert len(res["outputs"][0]["token_ids"]) == 3
 
 
-def test_engine_megakernel_warns_on_long_max_model_len():
+def test_engine_megakernel_warns_on_long_max_model_len(tmp_path):
     from nanovllm import LLM
     from nanovllm.synthetic import write_model_dir
 
-    path = write_model_dir(os.path.join(ROOT, "_work", "test_model_2l"), num_layers=2)
+    path = write_model_dir(str(tmp_path / "model_2l"), num_layers=2)
     with pytest.warns(RuntimeWarning, match="requires max_model_len <= 2048"):
         LLM(path, max_model_len=4096, num_kvcache_blocks=4, decode_backend="megakernel")
 

@@ -153,11 +153,11 @@ def test_decode_step_matches_huggingface_qwen3():
     assert int(logits[0].float().argmax()) == int(ref.argmax())
 
 
-def test_package_torch_path_matches_oracle_first_tokens():
+def test_package_torch_path_matches_oracle_first_tokens(tmp_path):
     from nanovllm import LLM, SamplingParams
     from nanovllm.synthetic import write_model_dir
 
-    path = write_model_dir(os.path.join(ROOT, "_work", "test_model_2l"), num_layers=2)
+    path = write_model_dir(str(tmp_path / "model_2l"), num_layers=2)
     llm = LLM(path, max_model_len=2048, num_kvcache_blocks=4, decode_backend="torch")
     out = llm.generate([[1, 2, 3, 4, 5, 6, 7, 8]], SamplingParams(temperature=0.0, max_tokens=4, ignore_eos=True))
     oracle = orc.Oracle(synthetic_weights(2))
