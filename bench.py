@@ -218,7 +218,6 @@ def fusion_sweep(steps: int, warmup: int) -> dict:
     import torch
 
     out = {}
-    synth = None
     for g in (1, 2, 4, 7, 14, 28):
         _, _, _, dec = build_decoder(num_blocks=72, fusion_groups=g)
         for b in (1, 8):
