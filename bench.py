@@ -205,7 +205,7 @@ def long_context_runs(workload: str, steps: int, warmup: int) -> dict:
             out[f"{mode}_b{b}"] = {"us_per_step": round(us, 2), "tok_per_s": round(b / us * 1e6, 1),
                                    "GBps": round(nbytes / us / 1e3, 1),
                                    "floor_us": round(nbytes / HBM_PEAK_GBPS / 1e3, 2),
-                                   "splits": dec.splits_for(max(start) + steps + 1),
+                                   "splits": dec.splits_for(max(start) + steps + 1, b, mode),
                                    "ctx": [min(start) + 1, max(start) + steps]}
     dec.close()
     return out

@@ -7,8 +7,9 @@ Differences that matter:
 
 * one schedule per (batch bucket 1/2/4/8, split-KV factor); a live batch of 3,
   5, 6 or 7 runs the next bucket with the extra rows inactive;
-* the split-KV factor follows the context (one split per 256 positions, up to
-  16, never below ``megakernel_attn_splits``);
+* the split-KV factor follows the context and the batch (one split per 256
+  positions, never below ``megakernel_attn_splits``; for the tagged persistent
+  kernel at most 16 // batch bucket);
 * nothing is zeroed per step: the last LM-head task clears the fan-in
   counters and every ticket counter resets itself (the reference cleared about
   11.7 MB of scratch per step, ``taskgraph.py:289-295``);
@@ -289,8 +290,14 @@ class TaskGraphDecoder:
             raise native.MegakernelError(f"decode step failed on the device (error {err}: {kind})")
         return status[16:16 + rows].tolist()
 
-    def splits_for(self, max_context: int) -> int:
-        return auto_attn_splits(max_context, self.min_attn_splits)
+    def splits_for(self, max_context: int, batch: int = 1, mode: str | None = None) -> int:
+        """Split-KV factor for a step. The tagged persistent kernel caps splits at
+        16 // batch bucket; the per-op stage kernels need many workgroups per launch
+        and keep one split per 256 positions (measured at C5, batch 8: 2358 us per step
+        with 8 splits, 2692 us with 2)."""
+
+        capped = (mode or self.launch) == "persistent" and self.persistent_variant == "tagged"
+        return auto_attn_splits(max_context, self.min_attn_splits, batch_bucket(batch) if capped else 1)
 
     # -- decode ----------------------------------------------------------------
     def decode_rows(self, input_ids, positions, block_tables, active_rows=None, logits=None,
@@ -311,7 +318,7 @@ class TaskGraphDecoder:
             raise ValueError(
                 f"block table has {cols} columns but the task-graph page_table stride is "
                 f"{self.max_pages} (max_model_len // block_size)")
-        geo = self._geometry(batch_bucket(rows), self.splits_for(cols * self.block_size))
+        geo = self._geometry(batch_bucket(rows), self.splits_for(cols * self.block_size, rows, mode))
         self._ids[:rows].copy_(input_ids)
         self._seqlens[:rows].copy_(positions)
         self._table[:rows, :cols].copy_(block_tables)
@@ -369,7 +376,7 @@ class TaskGraphDecoder:
         """Return a zero-argument callable that runs one device-resident step
         (token fed back, position advanced on the device, no host sync)."""
 
-        geo = self._geometry(batch_bucket(rows), self.splits_for(max_context))
+        geo = self._geometry(batch_bucket(rows), self.splits_for(max_context, rows, mode))
         desc = self._desc_for(rows, geo, flags=native.FLAG_ADVANCE)
         if mode == "graph":
             handle = native.ctypes.c_void_p()

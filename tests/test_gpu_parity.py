@@ -232,7 +232,7 @@ def test_split_kv_long_ragged_context(mode, variant):
     err = max_abs(logits, ref_logits)
     err_torch = max_abs(torch_logits, ref_logits)
     bound = LOGIT_TOL + 1.5 * err_torch
-    print(f"  splits={h.dec.splits_for(8 * 256)} max|dlogit| {err:.3e} torch {err_torch:.3e} bound {bound:.3e} "
+    print(f"  splits={h.dec.splits_for(8 * 256, len(ids), mode)} max|dlogit| {err:.3e} torch {err_torch:.3e} bound {bound:.3e} "
           f"tokens {toks} {ref_toks}", flush=True)
     assert err <= bound
     check_tokens(toks, ref_toks, ref_logits, bound)

@@ -97,6 +97,10 @@ def test_buckets_and_auto_splits():
     assert auto_attn_splits(1) == 1 and auto_attn_splits(256) == 1 and auto_attn_splits(257) == 2
     assert auto_attn_splits(2048) == 8 and auto_attn_splits(10 ** 6) == 16
     assert auto_attn_splits(100, minimum=4) == 4
+    # batch cap: batch x splits <= 16, the minimum still wins
+    assert [auto_attn_splits(2048, batch=b) for b in (1, 2, 4, 8)] == [8, 8, 4, 2]
+    assert auto_attn_splits(10 ** 6, batch=2) == 8 and auto_attn_splits(300, batch=8) == 2
+    assert auto_attn_splits(200, batch=8) == 1 and auto_attn_splits(2048, minimum=8, batch=8) == 8
 
 
 @pytest.mark.parametrize("batch", [1, 2, 4, 8])
