@@ -145,3 +145,58 @@ def test_scheduler_batches_and_preempts(tmp_path):
         sched.postprocess(picked, [9] * len(picked), False)
     assert sched.block_manager.stats()["allocated_blocks"] <= 3
     assert any(s.status.name == "WAITING" for s in seqs) or prefill
+
+
+def test_safetensors_checkpoint_round_trip(tmp_path):
+    """The checkpoint loader (reference ``utils/loader.py:12-28``) reads Hugging Face
+    names. q/k/v and gate/up are separate tensors there, and it packs them into the
+    fused projections. The synthetic model is written as such a checkpoint, with the
+    fused tensors split and the tied ``lm_head.weight`` included. Loaded back, it must
+    give bit-identical parameters and the same greedy tokens."""
+    import shutil
+
+    import torch
+    from safetensors.torch import save_file
+
+    from nanovllm import LLM, SamplingParams
+    from nanovllm.synthetic import write_model_dir
+
+    src = write_model_dir(str(tmp_path / "synthetic"), num_layers=2)
+    ref = LLM(src, max_model_len=2048, num_kvcache_blocks=4, decode_backend="torch")
+    model = ref.model_runner.model
+    attn = model.model.layers[0].self_attn
+    tensors = {}
+    for name, p in model.named_parameters():
+        t = p.detach().cpu().contiguous()
+        if "qkv_proj" in name:
+            q, k, v = t.split([attn.q_size, attn.kv_size, attn.kv_size])
+            for short, part in (("q_proj", q), ("k_proj", k), ("v_proj", v)):
+                tensors[name.replace("qkv_proj", short)] = part.contiguous()
+        elif "gate_up_proj" in name:
+            g, u = t.chunk(2)
+            tensors[name.replace("gate_up_proj", "gate_proj")] = g.contiguous()
+            tensors[name.replace("gate_up_proj", "up_proj")] = u.contiguous()
+        else:
+            tensors[name] = t
+    tensors["lm_head.weight"] = model.model.embed_tokens.weight.detach().cpu().clone()
+    assert any(k.endswith("self_attn.k_proj.weight") for k in tensors)
+    ckpt = tmp_path / "checkpoint"
+    ckpt.mkdir()
+    shutil.copy(os.path.join(src, "config.json"), ckpt / "config.json")
+    names = sorted(tensors)
+    half = len(names) // 2   # two shards, as multi-file checkpoints have
+    save_file({k: tensors[k] for k in names[:half]}, str(ckpt / "model-00001-of-00002.safetensors"))
+    save_file({k: tensors[k] for k in names[half:]}, str(ckpt / "model-00002-of-00002.safetensors"))
+
+    loaded = LLM(str(ckpt), max_model_len=2048, num_kvcache_blocks=4, decode_backend="torch")
+    got = dict(loaded.model_runner.model.named_parameters())
+    for name, p in model.named_parameters():
+        assert torch.equal(p.detach().cpu(), got[name].detach().cpu()), name
+    sp = SamplingParams(temperature=0.0, max_tokens=4, ignore_eos=True)
+    prompts = [[11, 22, 33, 44, 55], [7] * 20]
+    assert loaded.generate(prompts, sp) == ref.generate(prompts, sp)
+    empty = tmp_path / "no_weights"
+    empty.mkdir()
+    shutil.copy(os.path.join(src, "config.json"), empty / "config.json")
+    with pytest.raises(FileNotFoundError, match="no safetensors"):
+        LLM(str(empty), max_model_len=2048, num_kvcache_blocks=4)
