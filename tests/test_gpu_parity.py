@@ -240,6 +240,36 @@ def test_split_kv_long_ragged_context(mode, variant):
     h.close()
 
 
+@pytest.mark.parametrize("mode,variant", [("persistent", "tagged"), ("graph", "lds_dma")])
+def test_batch8_long_ragged_context(mode, variant):
+    """Eight rows with ragged contexts up to 2000 on scattered pages. The tagged
+    kernel runs 2 splits here (batch-capped, ~1000 positions per split), and the
+    per-op path runs 8. Checked against the oracle with the torch-relative bound."""
+    print(f"case: batch 8 long ragged context, mode={mode} variant={variant}", flush=True)
+    h = Harness(num_layers=2, num_blocks=40, kv_fill_seed=5, launch=mode, variant=variant)
+    h.kv_before = h.kv_cpu.clone()
+    pos = [1800, 1500, 1023, 700, 300, 1999, 64, 1200]
+    ids = [3, 151935, 42, 9000, 123, 77777, 5, 60000]
+    perm = torch.randperm(40, generator=torch.Generator().manual_seed(7)).tolist()
+    tables = []
+    for p in pos:
+        n = p // 256 + 1
+        tables.append(perm[:n])
+        perm = perm[n:]
+    toks, logits = h.step(ids, pos, tables)
+    ref_toks, ref_logits = h.oracle_step(ids, pos, tables)
+    torch_logits = _torch_path_logits(2, h.kv_before, ids, pos, tables)
+    err = max_abs(logits, ref_logits)
+    err_torch = max_abs(torch_logits, ref_logits)
+    bound = LOGIT_TOL + 1.5 * err_torch
+    print(f"  splits={h.dec.splits_for(8 * 256, 8, mode)} max|dlogit| {err:.3e} torch {err_torch:.3e} "
+          f"bound {bound:.3e} tokens {toks} {ref_toks}", flush=True)
+    assert err <= bound
+    check_tokens(toks, ref_toks, ref_logits, bound)
+    check_kv(h)
+    h.close()
+
+
 @pytest.mark.parametrize("variant", VARIANTS)
 def test_greedy_decode_sixteen_steps_matches_oracle(variant):
     """C3-style autoregressive greedy decode (2 layers): the token sequence matches."""
