@@ -13,7 +13,8 @@ persistent decode kernel's algorithmic bytes per launch over its average
 launch duration from HIP events recorded around every launch of the timed
 region (same stream); cpu_baseline = the CPU oracle timed on a bounded sample
 on this host. Extra keys: per-mode and per-batch ("sweep") device us/step of
-the persistent kernel vs the captured per-op hipGraph, same kernels.
+the persistent kernel vs the captured per-op hipGraph, same kernels, at short
+context and ("sweep_long_c5") at the C5 long contexts.
 
 One GPU only: --gpus N > 1 exits with a message.
 """
@@ -179,7 +180,7 @@ def copy_calibration(nbytes: int = 1 << 30, launches: int = 4):
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "launches": launches}))
 
 
-def long_context_runs(workload: str, steps: int, warmup: int) -> dict:
+def long_context_runs(workload: str, steps: int, warmup: int, dec=None) -> dict:
     """C4 (batch 8, 512-token prompts) or C5 (batch 1/2/4/8, prompt lengths
     U[1024,1920], ragged block tables): device us/step of the persistent kernel
     and of the captured per-op hipGraph, same kernels, same inputs. The cache holds
@@ -189,7 +190,9 @@ def long_context_runs(workload: str, steps: int, warmup: int) -> dict:
     import random
 
     num_blocks = 8 * 8 + 8
-    _, _, _, dec = build_decoder(num_blocks=num_blocks)
+    own = dec is None
+    if own:
+        _, _, _, dec = build_decoder(num_blocks=num_blocks)
     rng = random.Random(0)
     if workload == "c4":
         cases = [(8, [512] * 8)]
@@ -207,7 +210,8 @@ def long_context_runs(workload: str, steps: int, warmup: int) -> dict:
                                    "floor_us": round(nbytes / HBM_PEAK_GBPS / 1e3, 2),
                                    "splits": dec.splits_for(max(start) + steps + 1, b, mode),
                                    "ctx": [min(start) + 1, max(start) + steps]}
-    dec.close()
+    if own:
+        dec.close()
     return out
 
 
@@ -328,6 +332,8 @@ def main():
                 sweep[f"{mode}_b{b}"] = {"us_per_step": round(us, 2), "tok_per_s": round(b / us * 1e6, 1),
                                          "GBps": round(sum(step_bytes(c) for c in ctxs) / len(ctxs) / us / 1e3, 1)}
         result["sweep"] = sweep
+        # C5 (prompt lengths U[1024,1920], ragged tables): the same boundary at long context
+        result["sweep_long_c5"] = long_context_runs("c5", 32, 4, dec=dec)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     dec.close()
