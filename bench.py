@@ -235,6 +235,40 @@ def fusion_sweep(steps: int, warmup: int) -> dict:
     return out
 
 
+def engine_runs(batch: int = 8, prompt_len: int = 512, max_tokens: int = 128) -> dict:
+    """The plugin end to end: ``LLM.generate`` with ``decode_backend="megakernel"``
+    and with ``"torch"`` on the same GPU (C4 shape by default). It includes the torch
+    prefill, the scheduler, per-step host staging and the one device-to-host read
+    per step. Reports the median decode-step wall time and decode tok/s."""
+
+    import random
+    import tempfile
+
+    import torch
+    from nanovllm import LLM, SamplingParams
+    from nanovllm.synthetic import write_model_dir
+
+    rng = random.Random(0)
+    prompts = [[rng.randrange(VOCAB) for _ in range(prompt_len)] for _ in range(batch)]
+    sp = SamplingParams(temperature=0.0, max_tokens=max_tokens, ignore_eos=True)
+    out = {}
+    with tempfile.TemporaryDirectory() as tmp:
+        path = write_model_dir(os.path.join(tmp, "qwen3_06b_synthetic"), num_layers=28)
+        for backend in ("megakernel", "torch"):
+            llm = LLM(path, max_model_len=2048, num_kvcache_blocks=8 * batch, max_num_seqs=8,
+                      decode_backend=backend)
+            llm.generate([p[:16] for p in prompts], SamplingParams(temperature=0.0, max_tokens=4, ignore_eos=True))
+            m = llm.generate_with_metrics(prompts, sp)["metrics"]
+            llm.exit()
+            del llm
+            torch.cuda.empty_cache()
+            step = m["decode_step_median_s"]
+            out[backend] = {"decode_step_median_us": round(step * 1e6, 1), "decode_tok_per_s": round(batch / step, 1),
+                            "decode_steps": m["decode_steps"], "decode_backends": m["decode_backends"],
+                            "fallback_reasons": m["fallback_reasons"], "wall_time_s": round(m["wall_time_s"], 3)}
+    return {"batch": batch, "prompt_len": prompt_len, "max_tokens": max_tokens, **out}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -254,6 +288,8 @@ def main():
                     help="cached positions per row before the first timed step (c3 path; the KV holds zeros)")
     ap.add_argument("--workload", default="c3", choices=["c3", "c4", "c5"],
                     help="c3: the headline line (default); c4/c5: long-context persistent vs hipGraph table")
+    ap.add_argument("--engine", action="store_true",
+                    help="LLM.generate end to end, megakernel vs torch decode backend (C4 shape)")
     ap.add_argument("--fusion-sweep", action="store_true",
                     help="persistent kernel at fusion_groups 1/2/4/7/14/28, batch 1 and 8")
     args = ap.parse_args()
@@ -269,6 +305,11 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.engine:
+        print(json.dumps({"metric": "engine decode step wall time and decode tok/s", "n_gpus": 1,
+                          "data": "synthetic (random-init bf16 weights seed 0, random prompts)",
+                          "engine": engine_runs()}))
         return
     if args.workload != "c3" or args.fusion_sweep:
         res = {"metric": "device us/decode-step & tok/s at batch 1-8 vs 1.19GB HBM weight floor", "unit": "us/step",

@@ -170,6 +170,15 @@ class MegakernelBackend:
         self._ensure_decoder()
         return self.decoder.decode_rows(input_ids, positions, block_tables)
 
+    def decode_seqs(self, seqs) -> list[int]:
+        """Batch step straight from the sequences (host values, pinned staging):
+        the runner's batch path. ``decode_batch`` keeps the device-tensor signature."""
+
+        self._ensure_decoder()
+        return self.decoder.decode_rows_host([s.last_token for s in seqs],
+                                             [decode_position(len(s)) for s in seqs],
+                                             [list(s.block_table) for s in seqs])
+
     def decode(self, seq, block_table) -> list[int]:
         self._ensure_decoder()
         return [int(self.decoder.step(seq.last_token, position=decode_position(len(seq)),

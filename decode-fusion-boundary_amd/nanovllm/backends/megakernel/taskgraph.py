@@ -187,9 +187,13 @@ class TaskGraphDecoder:
         self._mask_dirty = False
         self._table = torch.zeros(TG_MAX_BATCH, self.max_pages, **i32)
         self._logits = None
-        self._host_ids = torch.zeros(1, dtype=torch.int64, pin_memory=True)
-        self._host_pos = torch.zeros(1, dtype=torch.int32, pin_memory=True)
-        self._host_table = torch.zeros(self.max_pages, dtype=torch.int32, pin_memory=True)
+        # pinned staging for host-side steps (rows of decode_row / decode_rows_host);
+        # each step ends with a synchronous status read, so a step's copies have
+        # completed before the next step rewrites these buffers
+        self._host_ids = torch.zeros(TG_MAX_BATCH, dtype=torch.int64, pin_memory=True)
+        self._host_pos = torch.zeros(TG_MAX_BATCH, dtype=torch.int32, pin_memory=True)
+        self._host_tables = torch.zeros(TG_MAX_BATCH, self.max_pages, dtype=torch.int32, pin_memory=True)
+        self._host_table = self._host_tables[0]
 
         kv_stride = k_cache.stride(0)
         w = weights
@@ -342,8 +346,8 @@ class TaskGraphDecoder:
         self._host_ids[0] = int(token_id)
         self._host_pos[0] = int(position)
         self._host_table[:cols] = torch.as_tensor(table[:cols], dtype=torch.int32)
-        self._ids[:1].copy_(self._host_ids, non_blocking=True)
-        self._seqlens[:1].copy_(self._host_pos, non_blocking=True)
+        self._ids[:1].copy_(self._host_ids[:1], non_blocking=True)
+        self._seqlens[:1].copy_(self._host_pos[:1], non_blocking=True)
         self._table[0, :cols].copy_(self._host_table[:cols], non_blocking=True)
         if self._mask_dirty:
             self._row_active.fill_(1)
@@ -351,6 +355,43 @@ class TaskGraphDecoder:
         geo = self._geometry(1, self.splits_for(cols * self.block_size))
         self._launch(self._desc_for(1, geo), geo)
         return int(self._read_status(1)[0])
+
+    def decode_rows_host(self, input_ids: list[int], positions: list[int], block_tables: list[list[int]]) -> list[int]:
+        """One step for every row from host lists (the engine's batch path). Same
+        contract as :meth:`decode_rows`, but the rows are packed into pinned host
+        buffers and copied without blocking, instead of being built as device
+        tensors first."""
+
+        rows = len(input_ids)
+        if rows == 0:
+            return []
+        if rows > TG_MAX_BATCH:
+            raise RuntimeError(
+                f"decode_rows got {rows} rows but this decoder is sized for {TG_MAX_BATCH} (TG_MAX_BATCH); "
+                "the backend's compatibility check should have rejected this batch upstream")
+        if len(positions) != rows or len(block_tables) != rows:
+            raise ValueError("input_ids, positions and block_tables must have one entry per row")
+        cols = max(len(t) for t in block_tables)
+        if cols > self.max_pages:
+            raise ValueError(
+                f"block table has {cols} columns but the task-graph page_table stride is "
+                f"{self.max_pages} (max_model_len // block_size)")
+        ids, pos, tab = self._host_ids.numpy(), self._host_pos.numpy(), self._host_tables.numpy()
+        for r in range(rows):
+            ids[r] = input_ids[r]
+            pos[r] = positions[r]
+            t = block_tables[r]
+            tab[r, :len(t)] = t
+            tab[r, len(t):cols] = 0
+        self._ids[:rows].copy_(self._host_ids[:rows], non_blocking=True)
+        self._seqlens[:rows].copy_(self._host_pos[:rows], non_blocking=True)
+        self._table[:rows, :cols].copy_(self._host_tables[:rows, :cols], non_blocking=True)
+        if self._mask_dirty:
+            self._row_active.fill_(1)
+            self._mask_dirty = False
+        geo = self._geometry(batch_bucket(rows), self.splits_for(cols * self.block_size, rows))
+        self._launch(self._desc_for(rows, geo), geo)
+        return self._read_status(rows)
 
     def step(self, token_id: int, position: int | None = None, block_table=None) -> int:
         if position is None or block_table is None:

@@ -201,8 +201,7 @@ class ModelRunner:
                     if len(seqs) == 1:
                         token_ids = self.megakernel.decode(seqs[0], seqs[0].block_table)
                     else:
-                        ids, pos, meta = self.prepare_decode(seqs)
-                        token_ids = self.megakernel.decode_batch(ids, pos, meta.block_tables)
+                        token_ids = self.megakernel.decode_seqs(seqs)
                 except Exception as exc:
                     if self.megakernel.decoder is not None:
                         self._cuda_poisoned = True

@@ -270,6 +270,27 @@ def test_batch8_long_ragged_context(mode, variant):
     h.close()
 
 
+def test_host_staged_rows_match_device_rows():
+    """``decode_rows_host`` (pinned host staging, the engine's batch path) gives the
+    same tokens and the same KV writes, bit for bit, as ``decode_rows`` on device
+    tensors, for 5 ragged rows (bucket 8) and then 1 row that rewrites the staging."""
+    print("case: host-staged rows vs device rows, 5 rows then 1", flush=True)
+    h = Harness(num_layers=2, num_blocks=16, kv_fill_seed=9, variant="tagged")
+    kv0 = h.kv.clone()
+    cases = [([11, 22, 33, 44, 55], [700, 3, 256, 1023, 90], [[1, 2, 3], [4], [5, 6], [7, 8, 9, 10], [11]]),
+             ([66], [300], [[12, 13]])]
+    for ids, pos, tables in cases:
+        h.kv.copy_(kv0)
+        dev_toks, _ = h.step(ids, pos, tables)
+        kv_dev = h.kv.clone()
+        h.kv.copy_(kv0)
+        host_toks = h.dec.decode_rows_host(ids, pos, tables)
+        torch.cuda.synchronize()
+        assert host_toks == dev_toks, (host_toks, dev_toks)
+        assert torch.equal(h.kv, kv_dev)
+    h.close()
+
+
 @pytest.mark.parametrize("variant", VARIANTS)
 def test_greedy_decode_sixteen_steps_matches_oracle(variant):
     """C3-style autoregressive greedy decode (2 layers): the token sequence matches."""
