@@ -181,19 +181,21 @@ class TaskGraphDecoder:
         i32 = dict(dtype=torch.int32, device=self.device)
         self._workspace = torch.zeros(int(self._lib.mkd_workspace_bytes()), dtype=torch.uint8, device=self.device)
         self._status_off = int(self._lib.mkd_status_offset())
-        self._ids = torch.zeros(TG_MAX_BATCH, dtype=torch.int64, device=self.device)
-        self._seqlens = torch.zeros(TG_MAX_BATCH, **i32)
+        # Per-step row inputs in one int32 buffer: token ids (int64, 16 words), positions
+        # (8 words), block tables (8 x max_pages words). A pinned host mirror of the same
+        # layout lets a host-side step stage all of them with one copy.
+        self._rows_words = 2 * TG_MAX_BATCH + TG_MAX_BATCH + TG_MAX_BATCH * self.max_pages
+        self._rows_dev = torch.zeros(self._rows_words, **i32)
+        self._ids, self._seqlens, self._table = self._row_views(self._rows_dev)
         self._row_active = torch.ones(TG_MAX_BATCH, **i32)
         self._mask_dirty = False
-        self._table = torch.zeros(TG_MAX_BATCH, self.max_pages, **i32)
         self._logits = None
-        # pinned staging for host-side steps (rows of decode_row / decode_rows_host);
-        # each step ends with a synchronous status read, so a step's copies have
-        # completed before the next step rewrites these buffers
-        self._host_ids = torch.zeros(TG_MAX_BATCH, dtype=torch.int64, pin_memory=True)
-        self._host_pos = torch.zeros(TG_MAX_BATCH, dtype=torch.int32, pin_memory=True)
-        self._host_tables = torch.zeros(TG_MAX_BATCH, self.max_pages, dtype=torch.int32, pin_memory=True)
-        self._host_table = self._host_tables[0]
+        # pinned staging for host-side steps (decode_row / decode_rows_host) and the
+        # status read; each step ends with a synchronous status read, so a step's
+        # copies have completed before the next step rewrites these buffers
+        self._rows_host = torch.zeros(self._rows_words, dtype=torch.int32, pin_memory=True)
+        self._host_ids, self._host_pos, self._host_tables = self._row_views(self._rows_host)
+        self._host_status = torch.zeros(32, dtype=torch.int32, pin_memory=True)
 
         kv_stride = k_cache.stride(0)
         w = weights
@@ -253,6 +255,18 @@ class TaskGraphDecoder:
         self._geometries[key] = geo
         return geo
 
+    def _row_views(self, buf):
+        """(ids int64 [8], positions int32 [8], tables int32 [8, max_pages]) views of a row buffer."""
+
+        n = TG_MAX_BATCH
+        return buf[:2 * n].view(torch.int64), buf[2 * n:3 * n], buf[3 * n:].view(n, self.max_pages)
+
+    def _stage_host_rows(self, rows: int) -> None:
+        """Copy the first ``rows`` rows of the pinned mirror to the device in one copy."""
+
+        n = 3 * TG_MAX_BATCH + rows * self.max_pages
+        self._rows_dev[:n].copy_(self._rows_host[:n], non_blocking=True)
+
     def _desc_for(self, rows: int, geo: _Geometry, flags: int = 0, logits=None) -> native.MkdStepDesc:
         d = native.MkdStepDesc.from_buffer_copy(self._desc)
         d.rows = rows
@@ -284,7 +298,10 @@ class TaskGraphDecoder:
             native.check(self._lib.mkd_graph_launch(geo.graph[1], stream))
 
     def _read_status(self, rows: int) -> list[int]:
-        status = self._workspace[self._status_off:self._status_off + 128].view(torch.int32).cpu()
+        self._host_status.copy_(self._workspace[self._status_off:self._status_off + 128].view(torch.int32),
+                                non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        status = self._host_status
         err = int(status[0])
         if err != 0:
             native.check(self._lib.mkd_reset_counters(native.ctypes.byref(self._desc), self._stream_ptr()))
@@ -345,10 +362,10 @@ class TaskGraphDecoder:
             raise ValueError(f"block table has {len(table)} pages but the stride is {self.max_pages}")
         self._host_ids[0] = int(token_id)
         self._host_pos[0] = int(position)
-        self._host_table[:cols] = torch.as_tensor(table[:cols], dtype=torch.int32)
-        self._ids[:1].copy_(self._host_ids[:1], non_blocking=True)
-        self._seqlens[:1].copy_(self._host_pos[:1], non_blocking=True)
-        self._table[0, :cols].copy_(self._host_table[:cols], non_blocking=True)
+        tab = self._host_tables.numpy()
+        tab[0, :cols] = table[:cols]
+        tab[0, cols:] = 0
+        self._stage_host_rows(1)
         if self._mask_dirty:
             self._row_active.fill_(1)
             self._mask_dirty = False
@@ -382,10 +399,8 @@ class TaskGraphDecoder:
             pos[r] = positions[r]
             t = block_tables[r]
             tab[r, :len(t)] = t
-            tab[r, len(t):cols] = 0
-        self._ids[:rows].copy_(self._host_ids[:rows], non_blocking=True)
-        self._seqlens[:rows].copy_(self._host_pos[:rows], non_blocking=True)
-        self._table[:rows, :cols].copy_(self._host_tables[:rows, :cols], non_blocking=True)
+            tab[r, len(t):] = 0
+        self._stage_host_rows(rows)
         if self._mask_dirty:
             self._row_active.fill_(1)
             self._mask_dirty = False
