@@ -178,6 +178,7 @@ class ModelRunner:
             is_prefill=False,
             slot_mapping=torch.tensor(slots, dtype=torch.int32, device=self.device),
             context_lens=torch.tensor(lens, dtype=torch.int32, device=self.device),
+            context_lens_host=lens,
             block_tables=self.prepare_block_tables(seqs),
         )
         ids = torch.tensor(input_ids, dtype=torch.int64, device=self.device)

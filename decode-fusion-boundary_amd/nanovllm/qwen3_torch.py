@@ -43,6 +43,8 @@ class AttentionMetadata:
     # decode (and prefix-cached prefill)
     context_lens: torch.Tensor | None = None
     block_tables: torch.Tensor | None = None
+    # host copy of context_lens (saves each layer a device-to-host read)
+    context_lens_host: list[int] | None = None
 
 
 class RMSNorm(nn.Module):
@@ -146,7 +148,7 @@ class Attention(nn.Module):
                     ki, vi = k[cq[i] : cq[i + 1]], v[cq[i] : cq[i + 1]]
                 outs.append(_attend(qi, ki, vi, self.scale, len_k - qi.shape[0]))
         else:
-            lens = meta.context_lens.tolist()
+            lens = meta.context_lens_host if meta.context_lens_host is not None else meta.context_lens.tolist()
             for b, length in enumerate(lens):
                 kb = self._gather(k_cache, meta.block_tables[b], length)
                 vb = self._gather(v_cache, meta.block_tables[b], length)
