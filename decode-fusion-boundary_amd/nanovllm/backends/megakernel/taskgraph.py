@@ -110,10 +110,27 @@ def _check_tagged_preconditions(segs) -> None:
     even offsets (a word carries two values of one task), at most 32 rows per
     block (its result tile), one query head per attention task, and an LM-head
     task on every workgroup of the last launch (the last LM slot advances the step counter once every workgroup has
-    read it)."""
+    read it). Every workgroup also runs exactly one QKV and one gate/up task per
+    layer of a launch: each keeps the residual stream in registers, updates it in
+    every RMSNorm prologue, and flips a buffer parity per such task. A schedule with
+    fewer QKV tasks than workgroups (32-row QKV blocks on 256 workgroups, measured)
+    stalls the kernel until its dependency wait times out."""
 
+    norm_ops = (native.OP_QKV, native.OP_GATEUP)
     for seg in segs:
-        for row in seg.rows:
+        layers = {t.layer for row in seg.rows for t in row if t.op in norm_ops}
+        want = {(op, layer): 1 for op in norm_ops for layer in layers}
+        for w, row in enumerate(seg.rows):
+            seen: dict[tuple[int, int], int] = {}
+            for t in row:
+                if t.op in norm_ops:
+                    seen[(t.op, t.layer)] = seen.get((t.op, t.layer), 0) + 1
+            if seen != want:
+                (op, layer), n = next(((k, seen.get(k, 0)) for k in sorted(set(want) | set(seen))
+                                       if seen.get(k, 0) != 1))
+                raise RuntimeError(
+                    f"workgroup {w} runs {n} tasks of op {op} in layer {layer}; the tagged exchange "
+                    "needs exactly one QKV and one gate/up task per workgroup per layer")
             for t in row:
                 if t.op in (native.OP_QKV, native.OP_OPROJ, native.OP_GATEUP, native.OP_DOWN):
                     # result-tile entries: GATEUP has 2 rows per channel, DOWN 2 partials per row

@@ -104,7 +104,7 @@ def test_buckets_and_auto_splits():
 
 
 @pytest.mark.parametrize("batch", [1, 2, 4, 8])
-@pytest.mark.parametrize("splits", [1, 4, 16])
+@pytest.mark.parametrize("splits", [1, 2, 4, 8, 16])
 def test_tagged_exchange_preconditions_at_256_cus(batch, splits):
     """Even GEMV row blocks of <= 32 rows, one query head per attention task and
     an LM task on every workgroup; the per-KV-head schedule is rejected."""
@@ -113,6 +113,25 @@ def test_tagged_exchange_preconditions_at_256_cus(batch, splits):
         _check_tagged_preconditions(build_segments(batch, splits, 256, 28, groups, q_head_tasks=True))
     with pytest.raises(RuntimeError, match="one query head"):
         _check_tagged_preconditions(build_segments(batch, splits, 256, 28, 1))
+
+
+def test_tagged_exchange_needs_one_norm_task_per_workgroup_per_layer():
+    """Each workgroup keeps the residual stream in registers through every RMSNorm
+    prologue. A row missing a QKV task, or holding two gate/up tasks, in a layer is
+    rejected on the host before any launch."""
+    from nanovllm.backends.megakernel.taskgraph import _check_tagged_preconditions
+    for op in (native.OP_QKV, native.OP_GATEUP):
+        segs = build_segments(1, 1, 256, 28, 1, q_head_tasks=True)
+        row = segs[0].rows[5]
+        i = next(k for k, t in enumerate(row) if t.op == op and t.layer == 3)
+        del row[i]
+        with pytest.raises(RuntimeError, match="exactly one QKV and one gate/up"):
+            _check_tagged_preconditions(segs)
+    segs = build_segments(1, 1, 256, 28, 1, q_head_tasks=True)
+    row = segs[0].rows[7]
+    row.append(next(t for t in row if t.op == native.OP_GATEUP))
+    with pytest.raises(RuntimeError, match="exactly one QKV and one gate/up"):
+        _check_tagged_preconditions(segs)
 
 
 def test_gate_up_publishes_residual_only_at_segment_ends():
