@@ -13,6 +13,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -149,30 +150,61 @@ int validate(const MkdStepDesc* d) {
   return MKD_OK;
 }
 
+// Per-device launch state of one persistent kernel: the dynamic-LDS attribute
+// is set and the co-residency bound measured on the first launch on a device.
+constexpr int MAX_DEVICES = 64;
+struct PkState {
+  bool ready = false;
+  int blocks_per_cu = 0;
+};
+std::mutex g_pk_mu;
+
+// Make `kern` launchable on the current device with `lds` bytes of dynamic LDS
+// and check that a grid of `grid` workgroups of `threads` can all be resident
+// at once (the persistent kernels' workgroups wait on each other, so a
+// workgroup that could not start would leave the others spinning until their
+// bounded waits give up).
+int pk_ready(PkState (&state)[MAX_DEVICES], const void* kern, int threads, int lds, int grid) {
+  int dev = 0, cus = 0;
+  MKD_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(MKD_E_INVALID, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_pk_mu);
+  PkState& st = state[dev];
+  if (!st.ready) {
+    if (lds > 0) MKD_HIP(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+    int nb = 0;
+    MKD_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, threads, (size_t)lds));
+    st.blocks_per_cu = nb;
+    st.ready = true;
+  }
+  MKD_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  if (st.blocks_per_cu < 1 || grid > cus * st.blocks_per_cu)
+    return fail(MKD_E_INVALID, "persistent grid of " + std::to_string(grid) + " workgroups cannot be co-resident: " +
+                                   std::to_string(cus) + " compute units x " + std::to_string(st.blocks_per_cu) +
+                                   " resident workgroups each");
+  return MKD_OK;
+}
+
 template <int B>
 int launch_persistent_b(const MkdStepDesc& d, const MkdSchedule& s, hipStream_t st) {
+  static PkState st_v1[MAX_DEVICES], st_tagged[MAX_DEVICES], st_dma[MAX_DEVICES];  // per instantiation
+  int rc = MKD_OK;
   if (d.flags & MKD_FLAG_PK_V1) {
+    rc = pk_ready(st_v1, reinterpret_cast<const void*>(k_persistent<B>), NT, 0, s.grid);
+    if (rc) return rc;
     hipLaunchKernelGGL(k_persistent<B>, dim3(s.grid), dim3(NT), 0, st, d, s);
   } else if (d.flags & MKD_FLAG_PK_TAGGED) {
     // its DMA waves stage 32-position KV chunks that must not straddle a cache block
     if (d.block_size % KV_CHUNK != 0)
       return fail(MKD_E_INVALID, "the tagged persistent kernel needs a block_size that is a multiple of 32");
-    static bool attr_set4 = false;  // per instantiation; set before the first launch
-    if (!attr_set4) {
-      MKD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_persistent4<B>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, PkCfg<B>::LDS_BYTES));
-      attr_set4 = true;
-    }
+    rc = pk_ready(st_tagged, reinterpret_cast<const void*>(k_persistent4<B>), PK_THREADS, PkCfg<B>::LDS_BYTES, s.grid);
+    if (rc) return rc;
     hipLaunchKernelGGL(k_persistent4<B>, dim3(s.grid), dim3(PK_THREADS), PkCfg<B>::LDS_BYTES, st, d, s);
   } else if (d.flags & MKD_FLAG_PK_V3) {
     return fail(MKD_E_INVALID, "the register-streaming persistent variant was removed");
   } else {
-    static bool attr_set = false;  // per instantiation; set before the first launch
-    if (!attr_set) {
-      MKD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k_persistent2<B>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, PkCfg<B>::LDS_BYTES));
-      attr_set = true;
-    }
+    rc = pk_ready(st_dma, reinterpret_cast<const void*>(k_persistent2<B>), PK_THREADS, PkCfg<B>::LDS_BYTES, s.grid);
+    if (rc) return rc;
     hipLaunchKernelGGL(k_persistent2<B>, dim3(s.grid), dim3(PK_THREADS), PkCfg<B>::LDS_BYTES, st, d, s);
   }
   MKD_HIP(hipGetLastError());
@@ -201,12 +233,6 @@ int do_persistent(const MkdStepDesc* d, const MkdSchedule* s, hipStream_t st) {
   if (rc) return rc;
   if (s == nullptr || s->inst == nullptr || s->num_inst == nullptr || s->grid < 1 || s->max_inst < 1)
     return fail(MKD_E_INVALID, "invalid persistent schedule");
-  int dev = 0, cus = 0;
-  MKD_HIP(hipGetDevice(&dev));
-  MKD_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  if (s->grid > cus)
-    return fail(MKD_E_INVALID, "persistent grid " + std::to_string(s->grid) + " exceeds the " +
-                                   std::to_string(cus) + " compute units (workgroups must be co-resident)");
   MkdStepDesc dd = *d;
   dd.flags |= MKD_FLAG_ZERO_FANIN;
   switch (d->batch) {
@@ -242,6 +268,7 @@ struct GraphHandle {
 };
 
 }  // namespace
+
 
 extern "C" {
 
