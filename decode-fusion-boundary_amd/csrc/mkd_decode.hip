@@ -267,8 +267,57 @@ struct GraphHandle {
   hipGraphExec_t exec = nullptr;
 };
 
+// After a step of the allocation-free entry point: copy the device error word
+// to the caller's status int and, when it is set, clear the counters and the
+// tagged exchange (error word last), so the next call starts clean. One
+// workgroup: every thread has read the error word before any clears it.
+__global__ __launch_bounds__(1024) void k_status_finish(uint8_t* ws, int32_t* status) {
+  uint32_t* ctr = reinterpret_cast<uint32_t*>(ws + OFF_CTR);
+  const uint32_t err = ld_co(ctr);
+  __syncthreads();
+  if (threadIdx.x == 0) *status = (int32_t)err;
+  if (err == 0u) return;
+  const int n = (int)((WORKSPACE_BYTES - OFF_CTR) / 4);
+  for (int i = 1 + threadIdx.x; i < n; i += blockDim.x) ctr[i] = 0u;
+  __syncthreads();
+  if (threadIdx.x == 0) st_co(ctr, 0u);
+}
+
 }  // namespace
 
+// Workspace of the allocation-free entry point (mkd_launch_persistent_noalloc):
+// one copy per device, WORKSPACE_BYTES (sized for the library's maxima: batch
+// 8, 28 layers, 16 attention splits, 1024 LM slots), held until the process
+// ends. Host code uses only the per-device address from hipGetSymbolAddress,
+// never this name.
+static __device__ __align__(256) uint8_t scratch[WORKSPACE_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// Address of this device's scratch, looked up (and cleared on `st`) on the
+// first call on the device.
+int scratch_for_device(hipStream_t st, void** out) {
+  int dev = 0;
+  MKD_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(MKD_E_INVALID, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    MKD_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (ptr == nullptr) return fail(MKD_E_HIP, "hipGetSymbolAddress returned a null scratch address");
+    uint32_t* ctr = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(ptr) + OFF_CTR);
+    hipLaunchKernelGGL(k_reset, dim3(256), dim3(256), 0, st, ctr, (int)((WORKSPACE_BYTES - OFF_CTR) / 4));
+    MKD_HIP(hipGetLastError());
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MKD_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -302,6 +351,27 @@ int mkd_reset_counters(const MkdStepDesc* d, void* stream) {
 
 int mkd_launch_persistent(const MkdStepDesc* d, const MkdSchedule* s, void* stream) {
   return do_persistent(d, s, (hipStream_t)stream);
+}
+
+int mkd_launch_persistent_noalloc(const MkdStepDesc* d, const MkdSchedule* s, int32_t* status, void* stream) {
+  if (d == nullptr) return fail(MKD_E_INVALID, "null step descriptor");
+  if (status == nullptr) return fail(MKD_E_INVALID, "null status pointer");
+  hipStream_t st = (hipStream_t)stream;
+  void* ws = nullptr;
+  int rc = scratch_for_device(st, &ws);
+  if (rc) return rc;
+  MkdStepDesc dd = *d;
+  dd.workspace = ws;
+  dd.workspace_bytes = WORKSPACE_BYTES;
+  const uint8_t* out_lo = reinterpret_cast<const uint8_t*>(d->out_tokens);
+  const uint8_t* ws_lo = reinterpret_cast<const uint8_t*>(ws);
+  if (out_lo >= ws_lo && out_lo < ws_lo + WORKSPACE_BYTES)
+    return fail(MKD_E_INVALID, "out_tokens must not point into the library's scratch");
+  rc = do_persistent(&dd, s, st);  // validates rows/batch/layers/slots against the scratch's maxima
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_status_finish, dim3(1), dim3(1024), 0, st, reinterpret_cast<uint8_t*>(ws), status);
+  MKD_HIP(hipGetLastError());
+  return MKD_OK;
 }
 
 int mkd_launch_stages(const MkdStepDesc* d, const int32_t* inst, const MkdStage* stages, int32_t n, void* stream) {

@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "mkd_status_offset",
     "mkd_reset_counters", "mkd_launch_persistent", "mkd_launch_stages",
     "mkd_check_error", "mkd_graph_create", "mkd_graph_launch", "mkd_graph_destroy",
+    "mkd_launch_persistent_noalloc",
 )
 
 
@@ -120,6 +121,9 @@ def _declare(lib) -> None:
     lib.mkd_reset_counters.argtypes = [P(MkdStepDesc), ctypes.c_void_p]
     lib.mkd_launch_persistent.restype = ctypes.c_int
     lib.mkd_launch_persistent.argtypes = [P(MkdStepDesc), P(MkdSchedule), ctypes.c_void_p]
+    lib.mkd_launch_persistent_noalloc.restype = ctypes.c_int
+    lib.mkd_launch_persistent_noalloc.argtypes = [P(MkdStepDesc), P(MkdSchedule), ctypes.c_void_p,
+                                                  ctypes.c_void_p]
     lib.mkd_launch_stages.restype = ctypes.c_int
     lib.mkd_launch_stages.argtypes = [P(MkdStepDesc), ctypes.c_void_p, P(MkdStage),
                                       ctypes.c_int32, ctypes.c_void_p]

@@ -166,6 +166,22 @@ int mkd_launch_stages(const MkdStepDesc* desc, const int32_t* inst,
 /* Read back the device error word (0 = ok); synchronizes `stream`. */
 int mkd_check_error(const MkdStepDesc* desc, void* stream, int32_t* code);
 
+/* Allocation-free variant of mkd_launch_persistent. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * descriptor's workspace/workspace_bytes are ignored; the step runs on a
+ * library-owned scratch array of mkd_workspace_bytes() bytes per device (sized
+ * for the maxima: batch 8, 28 layers, 16 attention splits, 1024 LM slots;
+ * larger descriptors are rejected), looked up and cleared on the first call on
+ * a device and held until the process ends. The caller passes inputs and
+ * outputs as usual (out_tokens must be its own device memory) plus `status`, a
+ * device int32 that receives the step's device error word (0 = ok); after an
+ * error the scratch is cleared for the next call. No hipMalloc/hipFree or
+ * allocating library call is made. All calls on one device share its scratch:
+ * calls that overlap on one GPU (several streams or threads) race. */
+int mkd_launch_persistent_noalloc(const MkdStepDesc* desc, const MkdSchedule* sched, int32_t* status,
+                                  void* stream);
+
 /* Captured hipGraph of either launch mode ("graph" comparator / replay path).
  * mode 0 = per-op stages, 1 = persistent. `steps` consecutive decode steps are
  * captured (use MKD_FLAG_ADVANCE to feed each step's token to the next). */
