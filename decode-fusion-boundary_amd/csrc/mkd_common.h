@@ -102,6 +102,14 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 }
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
+// Greedy-argmax order of torch.argmax: a NaN ranks above every number (the
+// first NaN wins), otherwise the larger value, and on equal values the lower
+// index. True when candidate (v, i) ranks above the current best (bv, bi).
+__device__ __forceinline__ bool lm_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  return vn ? (!bn || i < bi) : (!bn && (v > bv || (v == bv && i < bi)));
+}
+
 // a.lo*b.lo + a.hi*b.hi + c in fp32 (v_dot2_f32_bf16).
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),

@@ -191,9 +191,6 @@ __device__ __forceinline__ int dma_chunk(const WeightSrc& d, cint32_t* w, int j,
   }
   const int lane = threadIdx.x & 63;
   int n = 0;
-#ifdef MKD_PROBE_SKIP_DMA
-  return 0;
-#endif
   for (int u = dw; u < units; u += 4) {
     const int r = u / per_row, p = u % per_row;
     const uint16_t* row = base1 != nullptr ? ((r & 1) ? base1 : base0) + (size_t)(r >> 1) * stride
@@ -347,15 +344,12 @@ __device__ __forceinline__ void cw_chunk(const MkdStepDesc& d, const Ws& ws, con
       break;
     }
     case MKD_OP_LMHEAD: {
-#ifdef MKD_PROBE_SKIP_LM_COMPUTE
-      break;
-#endif
       uint16_t* logits = d.out_logits;
       chunk_gemv<B, H>(slot, nr, xs, [&](int r, const float* acc) {
         const float v = round_bf(pick_lane<B>(acc, lane));
         const int row = a0 + r0 + r;
         if (lane < B) {
-          if (v > best.v || (v == best.v && row < best.i)) { best.v = v; best.i = row; }
+          if (lm_better(v, row, best.v, best.i)) { best.v = v; best.i = row; }
           if (logits != nullptr && lane < d.rows) logits[(size_t)lane * V + row] = (uint16_t)f2bf(v);
         }
       });
@@ -379,7 +373,7 @@ __device__ __forceinline__ void cw_lm_epilogue(const MkdStepDesc& d, const Ws& w
     float v = bv[t]; int i = bi[t];
     for (int ww = 1; ww < PK_CW; ww++) {
       const float v2 = bv[ww * MAXB + t]; const int i2 = bi[ww * MAXB + t];
-      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+      if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
     }
     st_co(reinterpret_cast<uint64_t*>(ws.lmpart(w[MKD_I_A2]) + t),
           (uint64_t)__float_as_uint(v) | ((uint64_t)(uint32_t)i << 32));
@@ -399,12 +393,12 @@ __device__ __forceinline__ void cw_lm_epilogue(const MkdStepDesc& d, const Ws& w
     for (int s = lane; s < d.lm_slots; s += 64) {
       const uint64_t e = ld_co(reinterpret_cast<const uint64_t*>(ws.lmpart(s) + b));
       const float v2 = __uint_as_float((uint32_t)e); const int i2 = (int)(e >> 32);
-      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+      if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const float v2 = __shfl_xor(v, o, 64); const int i2 = __shfl_xor(i, o, 64);
-      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+      if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
     }
     if (lane == 0) {
       const int tok = i == 0x7fffffff ? 0 : i;
@@ -502,9 +496,6 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent2(MkdStepDesc d, Mk
       if (aborted) continue;  // keep pairing barriers with the DMA waves
       const uint8_t* slot = ring + (c % Cfg::NS) * SLOT_BYTES;
       if (op == MKD_OP_ATTN) {
-#ifdef MKD_PROBE_NO_ATTN
-        continue;
-#endif
         const bool produced = task_attn<B, SyncCW>(d, ws, w[MKD_I_LAYER], w[MKD_I_A0], w[MKD_I_A1], w[MKD_I_A2],
                                                    attn_smem, sync);
         if (produced && w[MKD_I_SIGNAL] >= 0) {

@@ -133,9 +133,6 @@ struct SyncLds {
   uint32_t* ctr;
   mutable uint32_t gen;  // barriers this wave has entered (every compute wave runs the same sequence)
   __device__ __forceinline__ void operator()() const {
-#ifdef MKD_PROBE_NO_SYNC  // measurement builds only (no-wait probes): the barrier costs nothing
-    return;
-#endif
     asm volatile("" ::: "memory");
     // the add needs no returned value: barrier k is complete when the counter
     // (4 adds per barrier) reaches 4 k, and the wave's own add, issued before
@@ -197,14 +194,8 @@ __device__ __forceinline__ void p4_trace_poll(const P4& c) {
 // a[] then waits only for loads issued before it.
 template <int N, class Addr>
 __device__ __forceinline__ void poll_issue(Addr addr, uint64_t (&a)[N]) {
-#ifdef MKD_PROBE_SKIP_POLL  // measurement builds only: no dependency waits at all (results are garbage)
-  (void)addr;
-#pragma unroll
-  for (int k = 0; k < N; k++) a[k] = 0;
-#else
 #pragma unroll
   for (int k = 0; k < N; k++) a[k] = ld_co(addr(k));
-#endif
 }
 // Check the first round and keep polling until every word carries `tag`
 // (one round in flight: measured no slower than two, with half the traffic;
@@ -213,12 +204,6 @@ template <int N, class Addr>
 __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_t (&v)[N], uint32_t tag,
                                             const Ws& ws) {
   static_assert(N <= 32, "pending mask");
-#ifdef MKD_PROBE_SKIP_POLL
-  (void)addr; (void)tag; (void)ws;
-#pragma unroll
-  for (int k = 0; k < N; k++) v[k] = a[k];
-  return true;
-#endif
   uint32_t pending = N == 32 ? ~0u : ((1u << N) - 1u);
   // The device error word and the clock are read only by a poll that has
   // already spun 62 rounds: the error word is loaded ahead of a round's polls
@@ -342,12 +327,7 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
   float s[B][4];
   bool ok = true;
   auto load_nw = [&]() {
-#ifdef MKD_PROBE_NO_NW  // measurement builds only: constant norm weights (no load)
-    (void)nw;
-    return make_uint2(0x3f803f80u, 0x3f803f80u);
-#else
     return ldg2u(nw + k0);
-#endif
   };
   uint2 wv;
   if (from_embed) {
@@ -597,7 +577,7 @@ __device__ __forceinline__ void chunk_lm_mfma(const uint8_t* slot, const uint4* 
   for (int i = 0; i < 4; i++) {
     const float acc = a0[i] + a1[i];
     const float v = valid ? round_bf(acc) : -INFINITY;
-    const bool better = v > lb.v[i] || (v == lb.v[i] && row < lb.i[i]);
+    const bool better = lm_better(v, row, lb.v[i], lb.i[i]);
     lb.v[i] = better ? v : lb.v[i];
     lb.i[i] = better ? row : lb.i[i];
     const int b = 4 * kg + i;
@@ -844,7 +824,7 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
           for (int o = 1; o < 16; o <<= 1) {
             const float v2 = __shfl_xor(v, o, 64);
             const int i2 = __shfl_xor(ix, o, 64);
-            const bool better = v2 > v || (v2 == v && i2 < ix);
+            const bool better = lm_better(v2, i2, v, ix);
             v = better ? v2 : v;
             ix = better ? i2 : ix;
           }
@@ -861,7 +841,7 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
 #pragma unroll
         for (int b = 0; b < B; b++) {
           const float v = round_bf(acc[b]);
-          const bool better = v > best.v[b] || (v == best.v[b] && row < best.i[b]);
+          const bool better = lm_better(v, row, best.v[b], best.i[b]);
           best.v[b] = better ? v : best.v[b];
           best.i[b] = better ? row : best.i[b];
         }
@@ -1006,7 +986,7 @@ __device__ __forceinline__ bool p4_lm_finish(const MkdStepDesc& d, const P4& c, 
     float v = bv[t]; int i = bi[t];
     for (int ww = 1; ww < PK_CW; ww++) {
       const float v2 = bv[ww * MAXB + t]; const int i2 = bi[ww * MAXB + t];
-      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+      if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
     }
     uint64_t* o = c.ws.tw(TW_LM + ((size_t)slot * MAXB + t) * 2);
     st_co(o, tw_make(__float_as_uint(v), tag));
@@ -1020,15 +1000,15 @@ __device__ __forceinline__ bool p4_lm_finish(const MkdStepDesc& d, const P4& c, 
       uint64_t e[2];
       ok = ok && poll_tagged<2>([&](int k) { return c.ws.tw(TW_LM + ((size_t)s * MAXB + b) * 2 + k); }, e, tag, c.ws);
       const float v2 = __uint_as_float((uint32_t)e[0]); const int i2 = (int)(uint32_t)e[1];
-      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+      if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const float v2 = __shfl_xor(v, o, 64); const int i2 = __shfl_xor(i, o, 64);
-      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+      if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
     }
     if (lane == 0) {
-      const int tok = i == 0x7fffffff ? 0 : i;  // all-NaN row: token 0
+      const int tok = i == 0x7fffffff ? 0 : i;  // (no candidate at all: token 0)
       d.out_tokens[b] = tok;
       if (d.flags & MKD_FLAG_ADVANCE) { d.input_ids[b] = tok; d.cache_seqlens[b] += 1; }
     }
@@ -1209,11 +1189,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   uint32_t wnw = 0;
   float c0 = 0.f, c1 = 0.f, s0 = 0.f, s1 = 0.f;
   if (wave < 2) {
-#ifdef MKD_PROBE_NO_NW
-    wnw = 0x3f803f80u;
-#else
     wnw = ldg(reinterpret_cast<const uint32_t*>(p4_wptr(d, layer, wave == 0 ? MKD_W_Q_NORM : MKD_W_K_NORM)) + lane);
-#endif
     const int j = (2 * lane) & 63;
     const float* cs = d.rope_cos + (size_t)pos * (HD / 2);
     const float* sn = d.rope_sin + (size_t)pos * (HD / 2);
@@ -1525,11 +1501,18 @@ __device__ __forceinline__ void dma_decode_attn(DmaTask& t, const uint8_t* karg,
   t.lds0 = g.c_end;
 }
 
-// KV chunk j of ATTN task t into `slot` (this DMA wave's 4 units).
-__device__ __forceinline__ void dma_issue_attn(const DmaTask& t, int j, uint8_t* slot, int dw) {
+// KV chunk j of ATTN task t into `slot` (this DMA wave's 4 units). A cached
+// position's block id outside [0, num_blocks) is reported as ERR_BAD_INPUT and
+// clamped, so no copy leaves the cache.
+__device__ __forceinline__ void dma_issue_attn(const DmaTask& t, int j, uint8_t* slot, int dw, const uint8_t* karg) {
   const int lane = threadIdx.x & 63;
   const int P0 = t.nfull + KV_CHUNK * j, bs = t.stride;
-  const int blk = min(max(t.table()[P0 / bs], 0), t.units - 1);
+  const int raw = t.table()[P0 / bs];
+  const int blk = min(max(raw, 0), t.units - 1);
+  if (raw != blk && lane == 0) {
+    const Ws ws{karg_field<uint8_t*>(karg, offsetof(MkdStepDesc, workspace))};
+    st_co(ws.line(CTR_ERR), ERR_BAD_INPUT);
+  }
   const size_t row0 = (size_t)blk * bs + P0 % bs;
   const int s16 = lane & 15;
 #pragma unroll
@@ -1614,7 +1597,6 @@ __device__ __forceinline__ void dma_issue(DmaTask& t, int j, uint8_t* slot, int 
   constexpr int UPC = (16 / PR) * PR;
   constexpr int LPW = UPC / 4;      // copies per DMA wave per chunk
   const int lane = threadIdx.x & 63;
-#ifndef MKD_PROBE_SKIP_DMA
   // lane i of the copy of a 1-KiB unit brings piece (i + r) mod 64 of it, r =
   // the unit's row within the chunk (wpiece): a rotation per row
   if (j < t.nfull) {
@@ -1641,9 +1623,6 @@ __device__ __forceinline__ void dma_issue(DmaTask& t, int j, uint8_t* slot, int 
     __builtin_amdgcn_global_load_lds((gbl_void_t*)(row + p * 512 + src_lane * 8), (lds_void_t*)(slot + (u - u0) * 1024),
                                      16, 0, 0);
   }
-#else
-  (void)t; (void)j; (void)slot; (void)dw; (void)lane;
-#endif
 }
 
 // s_waitcnt vmcnt(3 * later) for a runtime later in [0, M]: chunk r has landed
@@ -1715,7 +1694,7 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
     if (cur.kind == 0) dma_issue<H>(cur, tj, slot, dw);
     else if (cur.kind == 1) dma_issue<QS>(cur, tj, slot, dw);
     else if (cur.kind == 2) dma_issue<I>(cur, tj, slot, dw);
-    else dma_issue_attn(cur, tj, slot, dw);
+    else dma_issue_attn(cur, tj, slot, dw, karg);
     issued++;
     if (++tj == cur.nch) {
       tj = 0;

@@ -251,8 +251,13 @@ __device__ __forceinline__ bool task_attn(const MkdStepDesc& d, const Ws& ws, in
   //    (waves 0,1: q heads 2h, 2h+1; wave 2: k; wave 3: v copy)
   {
     const int n_pages = live ? min(pos / d.block_size + 1, MAX_PAGES) : 0;
-    for (int i = t; i < n_pages; i += NW * 64)
-      pages[i] = min(max(d.page_table[(size_t)b * d.page_stride + i], 0), d.num_blocks - 1);
+    for (int i = t; i < n_pages; i += NW * 64) {
+      // a block id outside the cache is reported and clamped (no access leaves the cache)
+      const int raw = d.page_table[(size_t)b * d.page_stride + i];
+      const int blk = min(max(raw, 0), d.num_blocks - 1);
+      if (raw != blk) st_co(ws.line(CTR_ERR), ERR_BAD_INPUT);
+      pages[i] = blk;
+    }
     const uint16_t* row = ws.qkv() + (size_t)b * QKV_N;
     if (wave < 4) {
     const uint16_t* src = wave < 2 ? row + (GROUP * h + wave) * HD : (wave == 2 ? row + QS + h * HD : row + QS + KVS + h * HD);
@@ -458,7 +463,7 @@ __device__ void task_lmhead(const MkdStepDesc& d, const Ws& ws, int r0, int nr, 
   gemv<B, H, 4>(rowptr, r0, nr, xs, [&](int r, const float* acc) {
     const float v = round_bf(pick_lane<B>(acc, lane));
     if (lane < B) {
-      if (v > best) { best = v; best_i = r; }  // rows arrive in increasing order per wave
+      if (lm_better(v, r, best, best_i)) { best = v; best_i = r; }
       if (logits != nullptr && lane < d.rows) logits[(size_t)lane * V + r] = (uint16_t)f2bf(v);
     }
   });
@@ -472,7 +477,7 @@ __device__ void task_lmhead(const MkdStepDesc& d, const Ws& ws, int r0, int nr, 
     float v = bv[t]; int i = bi[t];
     for (int w = 1; w < NWAVE; w++) {
       const float v2 = bv[w * MAXB + t]; const int i2 = bi[w * MAXB + t];
-      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+      if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
     }
     st_co(reinterpret_cast<uint64_t*>(ws.lmpart(slot) + t), (uint64_t)__float_as_uint(v) | ((uint64_t)(uint32_t)i << 32));
   }
@@ -492,15 +497,15 @@ __device__ void task_lmhead(const MkdStepDesc& d, const Ws& ws, int r0, int nr, 
     for (int s = lane; s < d.lm_slots; s += 64) {
       const uint64_t e = ld_co(reinterpret_cast<const uint64_t*>(ws.lmpart(s) + b));
       const float v2 = __uint_as_float((uint32_t)e); const int i2 = (int)(e >> 32);
-      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+      if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const float v2 = __shfl_xor(v, o, 64); const int i2 = __shfl_xor(i, o, 64);
-      if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+      if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
     }
     if (lane == 0) {
-      const int tok = i == 0x7fffffff ? 0 : i;  // all-NaN row: token 0
+      const int tok = i == 0x7fffffff ? 0 : i;  // (no candidate at all: token 0)
       d.out_tokens[b] = tok;
       if (d.flags & MKD_FLAG_ADVANCE) {
         d.input_ids[b] = tok;

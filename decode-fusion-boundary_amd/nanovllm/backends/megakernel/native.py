@@ -15,6 +15,7 @@ from pathlib import Path
 MKD_ABI_VERSION = 1
 MAX_BATCH = 8
 MAX_SPLITS = 16
+MAX_POSITION = 2048   # rows of the RoPE tables (MKD_MAX_POSITION)
 INST_WORDS = 8
 MAX_LM_SLOTS = 1024
 LAYER_PTRS = 11

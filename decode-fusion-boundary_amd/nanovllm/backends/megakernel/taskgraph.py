@@ -93,6 +93,36 @@ def taskgraph_compatibility(config: Any, seqs: list[Any], is_prefill: bool) -> T
     return TaskGraphCompatibility(True)
 
 
+def audit_rows(input_ids, positions, block_tables, *, block_size: int, num_blocks: int, max_model_len: int,
+               max_pages: int) -> None:
+    """Host audit of one step's rows (lists): at most 8 rows, token ids in the
+    vocabulary, each position inside ``max_model_len`` and covered by its block
+    table, and every block id the step reads or writes (pages ``0 .. position //
+    block_size``) inside the cache. Raises :class:`MegakernelError` naming the
+    first bad row."""
+
+    rows = len(input_ids)
+    if rows > TG_MAX_BATCH:
+        raise native.MegakernelError(f"{rows} rows exceed the batch ceiling {TG_MAX_BATCH}")
+    vocab = QWEN3_06B.vocab_size
+    limit = min(max_model_len, native.MAX_POSITION)
+    for r in range(rows):
+        tok, pos, table = int(input_ids[r]), int(positions[r]), block_tables[r]
+        if not 0 <= tok < vocab:
+            raise native.MegakernelError(f"row {r}: token id {tok} outside [0, {vocab})")
+        if not 0 <= pos < limit:
+            raise native.MegakernelError(f"row {r}: position {pos} outside [0, {limit})")
+        last = pos // block_size
+        if last >= len(table) or last >= max_pages:
+            raise native.MegakernelError(
+                f"row {r}: position {pos} needs page {last} but the block table has {len(table)} pages")
+        for i in range(last + 1):
+            blk = int(table[i])
+            if not 0 <= blk < num_blocks:
+                raise native.MegakernelError(
+                    f"row {r}: block id {blk} (page {i}) outside the cache's {num_blocks} blocks")
+
+
 @dataclass
 class _Geometry:
     batch: int
@@ -278,6 +308,25 @@ class TaskGraphDecoder:
         n = TG_MAX_BATCH
         return buf[:2 * n].view(torch.int64), buf[2 * n:3 * n], buf[3 * n:].view(n, self.max_pages)
 
+    def check_rows(self, input_ids, positions, block_tables) -> None:
+        """Host audit of one step's rows (:func:`audit_rows`). Runs on every
+        host-staged step; for device tensors only when ``debug_bounds`` is set
+        (reference ``taskgraph.py:419-420``)."""
+
+        audit_rows(input_ids, positions, block_tables, block_size=self.block_size,
+                   num_blocks=self.num_cache_blocks, max_model_len=self.max_model_len, max_pages=self.max_pages)
+
+    def _audit_device_rows(self, input_ids, positions, block_tables, geo: "_Geometry") -> None:
+        """``debug_bounds``: copy the rows to the host and audit them, and re-check
+        the launch's schedules (verifier and tagged-kernel preconditions)."""
+
+        self.check_rows(input_ids.tolist(), positions.tolist(), block_tables.tolist())
+        errors = verify(build_schedule(geo.batch, geo.attn_splits, self.grid, self.num_layers))
+        if errors:
+            raise native.MegakernelError("task-graph schedule failed verification: " + "; ".join(errors[:3]))
+        if self._variant_flags & native.FLAG_PK_TAGGED:
+            _check_tagged_preconditions(geo.segments)
+
     def _stage_host_rows(self, rows: int) -> None:
         """Copy the first ``rows`` rows of the pinned mirror to the device in one copy."""
 
@@ -293,13 +342,17 @@ class TaskGraphDecoder:
         d.out_logits = None if logits is None else logits.data_ptr()
         return d
 
-    def _launch(self, desc: native.MkdStepDesc, geo: _Geometry, mode: str | None = None) -> None:
+    def _launch(self, desc: native.MkdStepDesc, geo: _Geometry, mode: str | None = None,
+                on_segment=None) -> None:
         stream = self._stream_ptr()
         mode = mode or self.launch
         if mode == "persistent":
-            for _, _, sched in geo.persistent:
+            for i, (_, _, sched) in enumerate(geo.persistent):
                 native.check(self._lib.mkd_launch_persistent(native.ctypes.byref(desc),
                                                              native.ctypes.byref(sched), stream))
+                if on_segment is not None:
+                    torch.cuda.current_stream(self.device).synchronize()
+                    on_segment(i, geo.segments[i])
         elif mode == "stages":
             native.check(self._lib.mkd_launch_stages(native.ctypes.byref(desc), geo.stage_inst.data_ptr(),
                                                      geo.stages, geo.num_stages, stream))
@@ -339,10 +392,12 @@ class TaskGraphDecoder:
 
     # -- decode ----------------------------------------------------------------
     def decode_rows(self, input_ids, positions, block_tables, active_rows=None, logits=None,
-                    mode: str | None = None) -> list[int]:
+                    mode: str | None = None, on_segment=None) -> list[int]:
         """One step for every row. ``input_ids``/``positions``: int64 device ``[rows]``
         (positions = pre-decode length); ``block_tables``: int32 device ``[rows, cols]``
-        padded with 0. ``logits`` (optional bf16 ``[rows, vocab]``) receives the logits."""
+        padded with 0. ``logits`` (optional bf16 ``[rows, vocab]``) receives the logits.
+        ``on_segment(i, schedule)`` (persistent launch, diagnostics) is called after
+        layer segment ``i`` has completed, with the workspace holding its outputs."""
 
         rows = int(input_ids.numel())
         if rows == 0:
@@ -357,6 +412,8 @@ class TaskGraphDecoder:
                 f"block table has {cols} columns but the task-graph page_table stride is "
                 f"{self.max_pages} (max_model_len // block_size)")
         geo = self._geometry(batch_bucket(rows), self.splits_for(cols * self.block_size, rows, mode))
+        if self.debug_bounds:
+            self._audit_device_rows(input_ids, positions, block_tables, geo)
         self._ids[:rows].copy_(input_ids)
         self._seqlens[:rows].copy_(positions)
         self._table[:rows, :cols].copy_(block_tables)
@@ -367,7 +424,7 @@ class TaskGraphDecoder:
         elif self._mask_dirty:
             self._row_active.fill_(1)
             self._mask_dirty = False
-        self._launch(self._desc_for(rows, geo, logits=logits), geo, mode)
+        self._launch(self._desc_for(rows, geo, logits=logits), geo, mode, on_segment)
         return self._read_status(rows)
 
     def decode_row(self, token_id: int, position: int, block_table) -> int:
@@ -377,6 +434,7 @@ class TaskGraphDecoder:
         cols = min(len(table), self.max_pages)
         if len(table) > self.max_pages:
             raise ValueError(f"block table has {len(table)} pages but the stride is {self.max_pages}")
+        self.check_rows([token_id], [position], [table])
         self._host_ids[0] = int(token_id)
         self._host_pos[0] = int(position)
         tab = self._host_tables.numpy()
@@ -410,6 +468,7 @@ class TaskGraphDecoder:
             raise ValueError(
                 f"block table has {cols} columns but the task-graph page_table stride is "
                 f"{self.max_pages} (max_model_len // block_size)")
+        self.check_rows(input_ids, positions, block_tables)
         ids, pos, tab = self._host_ids.numpy(), self._host_pos.numpy(), self._host_tables.numpy()
         for r in range(rows):
             ids[r] = input_ids[r]

@@ -103,11 +103,14 @@ def attention_one(q, keys, values, scale=HEAD_DIM ** -0.5):
 
 
 def argmax_first(values: torch.Tensor) -> int:
-    """Index of the first maximal element (``torch.argmax`` rule)."""
+    """Index of the first maximal element (``torch.argmax`` rule: a NaN ranks
+    above every number, so the first NaN wins when there is one)."""
 
     best, idx = None, -1
     flat = values.float().tolist()
     for i, v in enumerate(flat):
+        if v != v:
+            return i
         if best is None or v > best:
             best, idx = v, i
     return idx
@@ -158,35 +161,57 @@ class Oracle:
         ``act``, ``down``, ``resid_post``) for per-op comparisons.
         """
 
-        rows = len(input_ids)
-        active = [True] * rows if row_active is None else [bool(a) for a in row_active]
-        x = self.w.embed[torch.as_tensor(list(input_ids), dtype=torch.long)]
-        hidden, residual = x, None
+        hidden, residual = self.embed_rows(input_ids), None
         for l in range(self.num_layers):
-            w, w32 = self.w.layers[l], self.layers32[l]
-            h, residual = add_rms_norm(hidden, residual, w["ln_in"])
-            q = linear(h, w32["q"]).view(rows, NUM_Q_HEADS, HEAD_DIM)
-            k = linear(h, w32["k"]).view(rows, NUM_KV_HEADS, HEAD_DIM)
-            v = linear(h, w32["v"]).view(rows, NUM_KV_HEADS, HEAD_DIM)
-            if trace is not None:
-                trace["qkv"] = torch.cat([q.reshape(rows, -1), k.reshape(rows, -1), v.reshape(rows, -1)], -1)
-                trace["resid_in"] = residual
-            q = rms_norm(q.float(), w["q_norm"])
-            k = rms_norm(k.float(), w["k_norm"])
-            attn = []
-            for b in range(rows):
-                pos = int(positions[b])
-                qb = rope(q[b], self.cos[pos], self.sin[pos])
-                kb = rope(k[b], self.cos[pos], self.sin[pos])
-                attn.append(self._attention(l, qb, kb, v[b], k_cache, v_cache,
-                                            block_tables[b], pos, active[b]))
-            attn_flat = torch.stack(attn).reshape(rows, -1)
-            o = linear(attn_flat, w32["o"])
-            h, residual = add_rms_norm(o, residual, w["ln_post"])
-            act = silu_mul(linear(h, w32["gate"]), linear(h, w32["up"]))
-            hidden = linear(act, w32["down"])
-            if trace is not None:
-                trace.update(attn=attn_flat, o=o, act=act, down=hidden, resid_post=residual)
+            hidden, residual = self.layer(l, hidden, residual, positions, block_tables, k_cache, v_cache,
+                                          row_active=row_active, trace=trace)
+        return self.head(hidden, residual)
+
+    def embed_rows(self, input_ids) -> torch.Tensor:
+        """bf16 embedding rows of the step's token ids (``models/qwen3.py:177-181``)."""
+
+        return self.w.embed[torch.as_tensor(list(input_ids), dtype=torch.long)]
+
+    def layer(self, l, hidden, residual, positions, block_tables, k_cache, v_cache,
+              row_active=None, trace: dict | None = None):
+        """Decoder layer ``l`` (``models/qwen3.py:147-160``) on bf16 ``hidden`` and
+        ``residual`` (``None`` at layer 0): returns ``(down output, residual after
+        the post-attention add)``, the pair the next layer (or the final norm)
+        adds. Writes the rows' K/V into the caches where the step writes them."""
+
+        rows = hidden.shape[0]
+        active = [True] * rows if row_active is None else [bool(a) for a in row_active]
+        w, w32 = self.w.layers[l], self.layers32[l]
+        h, residual = add_rms_norm(hidden, residual, w["ln_in"])
+        q = linear(h, w32["q"]).view(rows, NUM_Q_HEADS, HEAD_DIM)
+        k = linear(h, w32["k"]).view(rows, NUM_KV_HEADS, HEAD_DIM)
+        v = linear(h, w32["v"]).view(rows, NUM_KV_HEADS, HEAD_DIM)
+        if trace is not None:
+            trace["qkv"] = torch.cat([q.reshape(rows, -1), k.reshape(rows, -1), v.reshape(rows, -1)], -1)
+            trace["resid_in"] = residual
+        q = rms_norm(q.float(), w["q_norm"])
+        k = rms_norm(k.float(), w["k_norm"])
+        attn = []
+        for b in range(rows):
+            pos = int(positions[b])
+            qb = rope(q[b], self.cos[pos], self.sin[pos])
+            kb = rope(k[b], self.cos[pos], self.sin[pos])
+            attn.append(self._attention(l, qb, kb, v[b], k_cache, v_cache,
+                                        block_tables[b], pos, active[b]))
+        attn_flat = torch.stack(attn).reshape(rows, -1)
+        o = linear(attn_flat, w32["o"])
+        h, residual = add_rms_norm(o, residual, w["ln_post"])
+        gate, up = linear(h, w32["gate"]), linear(h, w32["up"])
+        act = silu_mul(gate, up)
+        hidden = linear(act, w32["down"])
+        if trace is not None:
+            trace.update(attn=attn_flat, o=o, gate=gate, up=up, act=act, down=hidden, resid_post=residual)
+        return hidden, residual
+
+    def head(self, hidden, residual):
+        """Final RMSNorm, tied LM head (bf16 logits) and greedy tokens
+        (``models/qwen3.py:183-187``, ``embed_head.py:56-66``, ``sampler.py:5-16``)."""
+
         h, _ = add_rms_norm(hidden, residual, self.w.final_norm)
         logits = linear(h, self.embed32)
         tokens = logits.float().argmax(dim=-1).tolist()

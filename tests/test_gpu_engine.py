@@ -83,3 +83,41 @@ def test_engine_megakernel_matches_torch_backend(tmp_path):
             full += first is None
             total += 1
     assert full >= MIN_FULL_FRACTION * total, f"{full} of {total} sequences agree on all tokens"
+
+
+def test_c4_agreement_megakernel_vs_torch_engine(tmp_path):
+    """C4 shape: 8 prompts of 512 random ids, 128 greedy tokens each, through the
+    engine on both decode backends (same GPU, same torch prefill). Classified by
+    the reference's PASS / CASCADE / FAIL rule and written to
+    ``gpurun_out/agreement_c4.json``; a FAIL (token 0 or a length differs) fails."""
+    import json
+    import os
+
+    from agreement import classify
+    from conftest import ROOT
+    from nanovllm import LLM, SamplingParams
+    from nanovllm.synthetic import write_model_dir
+
+    path = write_model_dir(str(tmp_path / "c4"), num_layers=28)
+    prompts = _prompts(4, [512] * 8)
+    sp = SamplingParams(temperature=0.0, max_tokens=128, ignore_eos=True)
+    tokens = {}
+    for backend in ("megakernel", "torch"):
+        llm = LLM(path, max_model_len=2048, num_kvcache_blocks=32, max_num_seqs=8, decode_backend=backend)
+        try:
+            r = llm.generate_with_metrics(prompts, sp)
+        finally:
+            llm.exit()
+        assert set(r["metrics"]["decode_backends"]) == {backend}, r["metrics"]["decode_backends"]
+        tokens[backend] = [o["token_ids"] for o in r["outputs"]]
+    status, details = classify(tokens["torch"], tokens["megakernel"])
+    agree = sum(a == b for x, y in zip(tokens["torch"], tokens["megakernel"]) for a, b in zip(x, y))
+    firsts = [d.get("first") for d in details]
+    print(f"  C4 status {status}: {agree}/{8 * 128} tokens agree; first divergences {firsts}", flush=True)
+    os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
+    with open(os.path.join(ROOT, "gpurun_out", "agreement_c4.json"), "w") as f:
+        json.dump({"config": "C4: 28 layers, 8 prompts x 512 random ids, 128 greedy tokens, megakernel engine "
+                             "vs torch engine on the same GPU", "status": status, "details": details,
+                   "tokens_agree": agree, "tokens_total": 8 * 128,
+                   "sequences_identical": 8 - len(details)}, f, indent=1)
+    assert status != "FAIL", details

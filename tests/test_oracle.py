@@ -113,6 +113,16 @@ def test_linear_silu_argmax():
     assert torch.equal(orc.silu_mul(a, b), (torch.nn.functional.silu(a.float()) * b.float()).to(torch.bfloat16))
     vals = torch.tensor([0.5, 2.0, -1.0, 2.0, 1.0])
     assert orc.argmax_first(vals) == 1 == int(torch.argmax(vals))
+    # NaN ranks above every number in torch.argmax; the first NaN wins
+    nan = float("nan")
+    for case in ([0.5, nan, 3.0, nan], [nan, 1.0], [1.0, 2.0, nan], [float("inf"), nan, 0.0]):
+        t = torch.tensor(case)
+        assert orc.argmax_first(t) == int(torch.argmax(t)), case
+    # the same rule over bf16 logits with exact ties spread through the array
+    g2 = torch.Generator().manual_seed(11)
+    for _ in range(50):
+        v = torch.randint(-3, 4, (300,), generator=g2).to(torch.bfloat16)
+        assert orc.argmax_first(v) == int(torch.argmax(v.float()))
 
 
 def _hf_qwen3(num_layers, weights):
