@@ -25,6 +25,9 @@ INCLUDE = REPO_ROOT / "include"
 LIB_NAME = "libmkd_decode.so"
 LIB_PATH = HERE / LIB_NAME
 SOURCES = ("mkd_decode.hip",)
+TORCH_OPS_NAME = "libmkd_torch_ops.so"
+TORCH_OPS_PATH = HERE / TORCH_OPS_NAME
+TORCH_OPS_SOURCE = "mkd_torch_ops.cpp"
 HEADERS = ("mkd_common.h", "mkd_tasks.h")
 
 
@@ -50,17 +53,46 @@ def compile_command(out: Path = LIB_PATH) -> list[str]:
     ]
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile the library (always; the caller decides when to rebuild)."""
+def torch_ops_command(out: Path = TORCH_OPS_PATH) -> list[str]:
+    """Host-only C++ compile of the torch operator shim against the installed
+    PyTorch-ROCm headers and libraries, linked to ``libmkd_decode.so`` (found
+    next to it at run time through ``$ORIGIN``)."""
 
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = compile_command(tmp)
+    import torch
+
+    tdir = Path(torch.__file__).resolve().parent
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    abi = int(torch.compiled_with_cxx11_abi())
+    return [
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+        "-D__HIP_PLATFORM_AMD__", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        f"-I{INCLUDE}", f"-I{tdir / 'include'}", f"-I{tdir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+        f"-I{rocm}/include",
+        "-o", str(out), str(CSRC / TORCH_OPS_SOURCE),
+        f"-L{HERE}", "-l:" + LIB_NAME, "-Wl,-rpath,$ORIGIN",
+        f"-L{tdir / 'lib'}", "-ltorch", "-ltorch_cpu", "-lc10", "-lc10_hip", "-ltorch_hip",
+        f"-Wl,-rpath,{tdir / 'lib'}", f"-L{rocm}/lib", "-lamdhip64",
+    ]
+
+
+def _run(cmd: list[str], out: Path, final: Path, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd))
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
-    os.replace(tmp, LIB_PATH)
+        raise RuntimeError(f"{cmd[0]} failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
+    os.replace(out, final)
+
+
+def build(verbose: bool = False, torch_ops: bool = True) -> Path:
+    """Compile the library and, unless ``torch_ops`` is False, the torch
+    operator shim (always; the caller decides when to rebuild)."""
+
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run(compile_command(tmp), tmp, LIB_PATH, verbose)
+    if torch_ops:
+        tmp = TORCH_OPS_PATH.with_suffix(".so.tmp")
+        _run(torch_ops_command(tmp), tmp, TORCH_OPS_PATH, verbose)
     return LIB_PATH
 
 

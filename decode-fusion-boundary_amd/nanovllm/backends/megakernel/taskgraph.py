@@ -180,8 +180,18 @@ class TaskGraphDecoder:
     def __init__(self, weights: dict, *, k_cache, v_cache, block_size: int, num_cache_blocks: int,
                  max_model_len: int, attn_splits: int = 1, fusion_groups: int = 1,
                  launch: str = "persistent", verbose: bool = False, debug_bounds: bool = False,
-                 persistent_variant: str = "tagged"):
+                 persistent_variant: str = "tagged", binding: str = "ctypes"):
         self._lib = native.load()
+        if binding not in ("ctypes", "torch_ops"):
+            raise ValueError(f"binding must be 'ctypes' or 'torch_ops'; got {binding!r}")
+        # how a persistent step reaches the library: ctypes calls of the C ABI, or
+        # the registered torch operator (torch.ops.nanovllm_megakernel_C.mkd_decode_step)
+        self.binding = binding
+        self._ops = None
+        if binding == "torch_ops":
+            from . import torch_ops
+
+            self._ops = torch_ops.load()
         if persistent_variant not in native.PERSISTENT_VARIANTS:
             raise ValueError(f"persistent_variant must be one of {sorted(native.PERSISTENT_VARIANTS)}; "
                              f"got {persistent_variant!r}")
@@ -228,6 +238,10 @@ class TaskGraphDecoder:
         i32 = dict(dtype=torch.int32, device=self.device)
         self._workspace = torch.zeros(int(self._lib.mkd_workspace_bytes()), dtype=torch.uint8, device=self.device)
         self._status_off = int(self._lib.mkd_status_offset())
+        # the status line's token slots (+64 bytes) as an int32 tensor: the tokens'
+        # destination when the step goes through the torch operator
+        self._op_tokens = self._workspace[self._status_off + 64:self._status_off + 128].view(torch.int32)
+        self._op_logits = None
         # Per-step row inputs in one int32 buffer: token ids (int64, 16 words), positions
         # (8 words), block tables (8 x max_pages words). A pinned host mirror of the same
         # layout lets a host-side step stage all of them with one copy.
@@ -347,9 +361,12 @@ class TaskGraphDecoder:
         stream = self._stream_ptr()
         mode = mode or self.launch
         if mode == "persistent":
-            for i, (_, _, sched) in enumerate(geo.persistent):
-                native.check(self._lib.mkd_launch_persistent(native.ctypes.byref(desc),
-                                                             native.ctypes.byref(sched), stream))
+            for i, (inst, num, sched) in enumerate(geo.persistent):
+                if self._ops is not None:
+                    self._launch_op(desc, inst, num, sched)
+                else:
+                    native.check(self._lib.mkd_launch_persistent(native.ctypes.byref(desc),
+                                                                 native.ctypes.byref(sched), stream))
                 if on_segment is not None:
                     torch.cuda.current_stream(self.device).synchronize()
                     on_segment(i, geo.segments[i])
@@ -366,6 +383,18 @@ class TaskGraphDecoder:
                     geo.num_stages, 1, stream, native.ctypes.byref(handle)))
                 geo.graph = ((desc.rows, desc.flags, desc.out_logits), handle)
             native.check(self._lib.mkd_graph_launch(geo.graph[1], stream))
+
+    def _launch_op(self, desc: native.MkdStepDesc, inst, num, sched: native.MkdSchedule) -> None:
+        """One persistent launch through the registered torch operator (same
+        descriptor fields as the ctypes call, passed as tensors)."""
+
+        w = self._weights
+        logits = self._op_logits if desc.out_logits else None
+        self._ops.mkd_decode_step(
+            self._layer_ptrs, w["embed"], w["final_norm"], w["cos"], w["sin"], self._k_cache, self._v_cache,
+            self._table, self._seqlens, self._row_active, self._ids, self._op_tokens, logits,
+            self._workspace, inst, num, sched.grid, sched.max_inst, desc.rows, desc.batch, desc.num_layers,
+            desc.lm_slots, desc.flags, self.num_cache_blocks, self.block_size)
 
     def _read_status(self, rows: int) -> list[int]:
         self._host_status.copy_(self._workspace[self._status_off:self._status_off + 128].view(torch.int32),
@@ -424,6 +453,7 @@ class TaskGraphDecoder:
         elif self._mask_dirty:
             self._row_active.fill_(1)
             self._mask_dirty = False
+        self._op_logits = logits
         self._launch(self._desc_for(rows, geo, logits=logits), geo, mode, on_segment)
         return self._read_status(rows)
 

@@ -1,11 +1,20 @@
-"""Paged-KV block allocator with xxhash prefix caching.
+"""Page pool of the paged KV cache, with prefix reuse of full pages.
 
-Behaviour follows the reference ``src/nanovllm/engine/block_manager.py:26-143``:
-full blocks are content-hashed (chained xxh64 over the previous block's hash
-and the block's token ids); a new prompt reuses cached full blocks whose
-tokens match; a decode appends a block exactly when the sequence length
-becomes ``1 (mod block_size)``.
+Pages are reference-counted. A page whose tokens are complete gets a content
+key (an xxh3 digest chained over the parent page's key and the page's token
+ids), so a later prompt with the same prefix maps those pages instead of
+recomputing them; a page freed by its last owner keeps its key until the pool
+hands it out again, so a finished request's prefix stays reusable for a while.
+Free pages are handed out oldest-freed first.
+
+Behaviour the rest of the engine relies on (reference
+``engine/block_manager.py:26-143``): a prompt occupies ``ceil(len / page)``
+pages; a decode step needs a new page exactly when the sequence length becomes
+``1 (mod page)``; releasing a sequence frees the pages no other sequence holds.
+The public name ``BlockManager`` and its ``stats()`` keys are kept for callers.
 """
+
+from __future__ import annotations
 
 from collections import deque
 
@@ -14,24 +23,16 @@ import xxhash
 
 from nanovllm.engine.sequence import Sequence
 
+NO_KEY = -1
 
-class Block:
-    __slots__ = ("block_id", "ref_count", "hash", "token_ids")
 
-    def __init__(self, block_id: int):
-        self.block_id = block_id
-        self.ref_count = 0
-        self.hash = -1
-        self.token_ids: list[int] = []
+def page_key(token_ids: list[int], parent: int = NO_KEY) -> int:
+    """Content key of a full page: xxh3-64 of the parent key and the token ids."""
 
-    def update(self, h: int, token_ids: list[int]) -> None:
-        self.hash = h
-        self.token_ids = token_ids
-
-    def reset(self) -> None:
-        self.ref_count = 1
-        self.hash = -1
-        self.token_ids = []
+    h = xxhash.xxh3_64()
+    h.update((parent & 0xFFFFFFFFFFFFFFFF).to_bytes(8, "little"))
+    h.update(np.asarray(token_ids, dtype=np.int32).tobytes())
+    return h.intdigest()
 
 
 class BlockManager:
@@ -39,121 +40,118 @@ class BlockManager:
         if num_blocks < 1:
             raise ValueError(f"num_blocks must be >= 1; got {num_blocks}")
         self.block_size = block_size
-        self.blocks = [Block(i) for i in range(num_blocks)]
-        self.hash_to_block_id: dict[int, int] = {}
-        self.free_block_ids: deque[int] = deque(range(num_blocks))
-        self.used_block_ids: set[int] = set()
-        self.prefix_cache_hits = 0
-        self.prefix_cache_misses = 0
-        self.freed_blocks = 0
-        self.peak_used_blocks = 0
+        self.num_blocks = num_blocks
+        self._refs = [0] * num_blocks                 # owners per page
+        self._key = [NO_KEY] * num_blocks             # content key per page (NO_KEY: none)
+        self._tokens: list[list[int] | None] = [None] * num_blocks
+        self._by_key: dict[int, int] = {}             # content key -> page
+        self._free: deque[int] = deque(range(num_blocks))
+        self._counts = {"prefix_cache_hits": 0, "prefix_cache_misses": 0, "freed_blocks": 0,
+                        "peak_used_blocks": 0}
 
-    @staticmethod
-    def compute_hash(token_ids: list[int], prefix: int = -1) -> int:
-        h = xxhash.xxh64()
-        if prefix != -1:
-            h.update(prefix.to_bytes(8, "little"))
-        h.update(np.asarray(token_ids, dtype=np.int64).tobytes())
-        return h.intdigest()
+    # -- pool primitives ---------------------------------------------------------
+    @property
+    def num_used(self) -> int:
+        return self.num_blocks - len(self._free)
 
-    def _take_block(self) -> int:
-        block_id = self.free_block_ids.popleft()
-        block = self.blocks[block_id]
-        if block.ref_count != 0:
-            raise RuntimeError(f"free block {block_id} still has references")
-        if block.hash != -1 and self.hash_to_block_id.get(block.hash) == block_id:
-            del self.hash_to_block_id[block.hash]
-        block.reset()
-        self.used_block_ids.add(block_id)
-        self.peak_used_blocks = max(self.peak_used_blocks, len(self.used_block_ids))
-        return block_id
+    def _hand_out(self) -> int:
+        page = self._free.popleft()
+        if self._refs[page]:
+            raise RuntimeError(f"page {page} on the free list still has owners")
+        self._forget(page)
+        self._refs[page] = 1
+        self._counts["peak_used_blocks"] = max(self._counts["peak_used_blocks"], self.num_used)
+        return page
 
-    def _release_block(self, block_id: int) -> None:
-        self.used_block_ids.remove(block_id)
-        self.free_block_ids.append(block_id)
-        self.freed_blocks += 1
+    def _forget(self, page: int) -> None:
+        key = self._key[page]
+        if key != NO_KEY and self._by_key.get(key) == page:
+            del self._by_key[key]
+        self._key[page] = NO_KEY
+        self._tokens[page] = None
 
-    def _cached_prefix(self, seq: Sequence) -> tuple[int, int]:
-        """(number of reusable full blocks, blocks that must come off the free list)."""
+    def _drop(self, page: int) -> None:
+        self._refs[page] -= 1
+        if self._refs[page] == 0:
+            self._free.append(page)
+            self._counts["freed_blocks"] += 1
 
-        h = -1
-        cached = 0
-        new_blocks = seq.num_blocks
+    def _lookup(self, key: int, tokens: list[int]) -> int:
+        page = self._by_key.get(key, -1)
+        return page if page >= 0 and self._tokens[page] == tokens else -1
+
+    def _reusable_prefix(self, seq: Sequence) -> list[int]:
+        """Pages holding the sequence's leading full pages, as far as they match.
+        The last page is never reused (its token is recomputed to get logits)."""
+
+        pages, key = [], NO_KEY
         for i in range(seq.num_blocks - 1):
             tokens = seq.block(i)
-            h = self.compute_hash(tokens, h)
-            block_id = self.hash_to_block_id.get(h, -1)
-            if block_id == -1 or self.blocks[block_id].token_ids != tokens:
+            key = page_key(tokens, key)
+            page = self._lookup(key, tokens)
+            if page < 0:
                 break
-            cached += 1
-            if block_id in self.used_block_ids:
-                new_blocks -= 1
-        return cached, new_blocks
+            pages.append(page)
+        return pages
 
+    # -- what the scheduler calls --------------------------------------------------
     def can_allocate(self, seq: Sequence) -> int:
-        """Number of prefix-cached blocks, or -1 when the pool is too small."""
+        """Leading pages reusable for ``seq``, or -1 when the free list cannot
+        supply the rest."""
 
-        cached, new_blocks = self._cached_prefix(seq)
-        return cached if len(self.free_block_ids) >= new_blocks else -1
+        reuse = self._reusable_prefix(seq)
+        fresh = seq.num_blocks - sum(1 for p in reuse if self._refs[p] > 0)
+        return len(reuse) if len(self._free) >= fresh else -1
 
     def allocate(self, seq: Sequence, num_cached_blocks: int) -> None:
+        """Give ``seq`` its pages: the first ``num_cached_blocks`` from the prefix
+        index (as :meth:`can_allocate` found them), the rest from the free list."""
+
         if seq.block_table:
             raise RuntimeError("sequence already owns blocks")
-        self.prefix_cache_hits += num_cached_blocks
-        self.prefix_cache_misses += max(0, seq.num_blocks - num_cached_blocks)
-        h = -1
-        for i in range(num_cached_blocks):
-            h = self.compute_hash(seq.block(i), h)
-            block_id = self.hash_to_block_id[h]
-            block = self.blocks[block_id]
-            if block_id in self.used_block_ids:
-                block.ref_count += 1
-            else:
-                block.ref_count = 1
-                self.free_block_ids.remove(block_id)
-                self.used_block_ids.add(block_id)
-            seq.block_table.append(block_id)
-        for _ in range(num_cached_blocks, seq.num_blocks):
-            seq.block_table.append(self._take_block())
-        seq.num_cached_tokens = num_cached_blocks * self.block_size
+        reuse = self._reusable_prefix(seq)[:num_cached_blocks]
+        if len(reuse) != num_cached_blocks:
+            raise RuntimeError("prefix pages changed between can_allocate and allocate")
+        for page in reuse:
+            if self._refs[page] == 0:
+                self._free.remove(page)       # revived from the free list
+            self._refs[page] += 1
+        self._counts["peak_used_blocks"] = max(self._counts["peak_used_blocks"], self.num_used)
+        seq.block_table.extend(reuse)
+        seq.block_table.extend(self._hand_out() for _ in range(seq.num_blocks - len(reuse)))
+        seq.num_cached_tokens = len(reuse) * self.block_size
+        self._counts["prefix_cache_hits"] += len(reuse)
+        self._counts["prefix_cache_misses"] += seq.num_blocks - len(reuse)
 
     def deallocate(self, seq: Sequence) -> None:
-        for block_id in reversed(seq.block_table):
-            block = self.blocks[block_id]
-            block.ref_count -= 1
-            if block.ref_count == 0:
-                self._release_block(block_id)
-        seq.num_cached_tokens = 0
+        for page in reversed(seq.block_table):
+            self._drop(page)
         seq.block_table.clear()
+        seq.num_cached_tokens = 0
 
     def can_append(self, seq: Sequence) -> bool:
-        needs_block = len(seq) % self.block_size == 1
-        return len(self.free_block_ids) >= int(needs_block)
+        """Whether the pool can cover the page the next decode step may need."""
+        return not self._needs_page(seq) or bool(self._free)
 
     def may_append(self, seq: Sequence) -> None:
-        if len(seq) % self.block_size == 1:
-            seq.block_table.append(self._take_block())
+        if self._needs_page(seq):
+            seq.block_table.append(self._hand_out())
+
+    def _needs_page(self, seq: Sequence) -> bool:
+        return len(seq) % self.block_size == 1
 
     def hash_blocks(self, seq: Sequence) -> None:
-        first = seq.num_cached_tokens // self.block_size
-        last = (seq.num_cached_tokens + seq.num_scheduled_tokens) // self.block_size
-        if first == last:
-            return
-        h = self.blocks[seq.block_table[first - 1]].hash if first > 0 else -1
-        for i in range(first, last):
-            block = self.blocks[seq.block_table[i]]
-            tokens = seq.block(i)
-            h = self.compute_hash(tokens, h)
-            block.update(h, tokens)
-            self.hash_to_block_id[h] = block.block_id
+        """Key the pages this step completes (after its tokens are cached)."""
+
+        done_before = seq.num_cached_tokens // self.block_size
+        done_after = (seq.num_cached_tokens + seq.num_scheduled_tokens) // self.block_size
+        key = self._key[seq.block_table[done_before - 1]] if done_before else NO_KEY
+        for i in range(done_before, done_after):
+            page, tokens = seq.block_table[i], seq.block(i)
+            key = page_key(tokens, key)
+            self._key[page], self._tokens[page] = key, tokens
+            self._by_key[key] = page
 
     def stats(self) -> dict[str, int]:
-        return {
-            "block_size": self.block_size,
-            "allocated_blocks": len(self.used_block_ids),
-            "free_blocks": len(self.free_block_ids),
-            "freed_blocks": self.freed_blocks,
-            "peak_used_blocks": self.peak_used_blocks,
-            "prefix_cache_hits": self.prefix_cache_hits,
-            "prefix_cache_misses": self.prefix_cache_misses,
-        }
+        return {"block_size": self.block_size, "allocated_blocks": self.num_used,
+                "free_blocks": len(self._free), **self._counts}

@@ -1,11 +1,22 @@
-"""Continuous-batching scheduler (reference ``src/nanovllm/engine/scheduler.py``).
+"""Continuous-batching scheduler: which sequences run in the next model step.
 
-Decode is preferred while prefill requests wait, for at most
-``prefill_decode_ratio`` consecutive decode steps; prefill is budgeted by
-``max_num_batched_tokens`` and ``max_prefill_tokens_per_step`` (chunked when a
-single prompt is larger); KV pressure preempts the most recently scheduled
-running sequence back to the waiting queue.
+Policy (the nano-vLLM engine's, reference ``engine/scheduler.py``):
+
+* a step is either a prefill step or a decode step, never both;
+* while sequences are decoding, decode steps are preferred, but after
+  ``prefill_decode_ratio`` decode steps in a row a waiting prompt gets a
+  prefill step (with nothing waiting, decode always runs);
+* a prefill step takes waiting prompts in arrival order under a token budget
+  of ``min(max_num_batched_tokens, max_prefill_tokens_per_step)``; the first
+  prompt of a step may be chunked to fit, later ones must fit whole; pages come
+  from the pool with prefix reuse, and a prompt whose pages do not fit waits;
+* a decode step takes up to ``max_num_seqs`` running sequences in order; when
+  the pool cannot give one its next page, the most recently admitted running
+  sequence is preempted (pages freed, back to the head of the waiting queue),
+  the sequence itself if it is the only one left.
 """
+
+from __future__ import annotations
 
 from collections import deque
 
@@ -18,130 +29,112 @@ class Scheduler:
     def __init__(self, config: Config):
         self.max_num_seqs = config.max_num_seqs
         self.max_num_batched_tokens = config.max_num_batched_tokens
-        self.max_prefill_tokens_per_step = (
-            config.max_prefill_tokens_per_step or config.max_num_batched_tokens
-        )
+        self.max_prefill_tokens_per_step = config.max_prefill_tokens_per_step or config.max_num_batched_tokens
         self.prefill_decode_ratio = config.prefill_decode_ratio
-        self._decode_steps_since_prefill = 0
         self.eos = config.eos
         self.block_size = config.kvcache_block_size
         self.block_manager = BlockManager(config.num_kvcache_blocks, config.kvcache_block_size)
         self.waiting: deque[Sequence] = deque()
         self.running: deque[Sequence] = deque()
-        self._peak_waiting = 0
-        self._peak_running = 0
+        self._decode_streak = 0          # decode steps since the last prefill step
+        self._peaks = {"waiting": 0, "running": 0}
 
-    def _note_peaks(self) -> None:
-        self._peak_waiting = max(self._peak_waiting, len(self.waiting))
-        self._peak_running = max(self._peak_running, len(self.running))
+    # -- queue state ---------------------------------------------------------------
+    def _track(self) -> None:
+        self._peaks["waiting"] = max(self._peaks["waiting"], len(self.waiting))
+        self._peaks["running"] = max(self._peaks["running"], len(self.running))
 
     def is_finished(self) -> bool:
-        return not self.waiting and not self.running
+        return not (self.waiting or self.running)
 
     def add(self, seq: Sequence) -> None:
         self.waiting.append(seq)
-        self._note_peaks()
+        self._track()
 
-    def _decode_first(self) -> bool:
-        return bool(self.running) and (
-            not self.waiting
-            or self._decode_steps_since_prefill < self.prefill_decode_ratio
-        )
-
+    # -- one step ------------------------------------------------------------------
     def schedule(self) -> tuple[list[Sequence], bool]:
-        self._note_peaks()
-        if self._decode_first():
-            seqs = self._schedule_decode()
-            if seqs:
-                self._decode_steps_since_prefill += 1
-                self._note_peaks()
-                return seqs, False
-        seqs = self._schedule_prefill()
-        if seqs:
-            self._decode_steps_since_prefill = 0
-            self._note_peaks()
-            return seqs, True
-        seqs = self._schedule_decode()
-        if seqs:
-            self._decode_steps_since_prefill += 1
-            self._note_peaks()
-            return seqs, False
+        """Returns ``(sequences, is_prefill)`` of the next step."""
+
+        self._track()
+        prefer_decode = bool(self.running) and (not self.waiting
+                                                or self._decode_streak < self.prefill_decode_ratio)
+        order = ((False, self._decode_batch), (True, self._prefill_batch))
+        for is_prefill, make in (order if prefer_decode else order[::-1]):
+            batch = make()
+            if batch:
+                self._decode_streak = 0 if is_prefill else self._decode_streak + 1
+                self._track()
+                return batch, is_prefill
         raise RuntimeError("scheduler made no progress")
 
-    def _schedule_prefill(self) -> list[Sequence]:
-        picked: list[Sequence] = []
+    def _prefill_batch(self) -> list[Sequence]:
+        pool = self.block_manager
+        budget = min(self.max_num_batched_tokens, self.max_prefill_tokens_per_step)
+        batch: list[Sequence] = []
         used = 0
-        budget = self.max_prefill_tokens_per_step
-        while self.waiting and len(picked) < self.max_num_seqs:
+        while self.waiting and len(batch) < self.max_num_seqs and used < budget:
             seq = self.waiting[0]
-            room = min(self.max_num_batched_tokens - used, budget - used)
-            if room == 0:
-                break
-            if not seq.block_table:
-                cached_blocks = self.block_manager.can_allocate(seq)
-                if cached_blocks == -1:
-                    break
-                todo = seq.num_tokens - cached_blocks * self.block_size
-            else:
-                todo = seq.num_tokens - seq.num_cached_tokens
-            if room < todo and picked:
-                break
-            if not seq.block_table:
-                self.block_manager.allocate(seq, cached_blocks)
+            has_pages = bool(seq.block_table)
+            reuse = 0
+            if not has_pages:
+                reuse = pool.can_allocate(seq)
+                if reuse < 0:
+                    break                                    # the pool cannot hold this prompt yet
+            todo = seq.num_tokens - (seq.num_cached_tokens if has_pages else reuse * self.block_size)
+            room = budget - used
+            if batch and room < todo:
+                break                                        # only a step's first prompt is chunked
+            if not has_pages:
+                pool.allocate(seq, reuse)
             seq.num_scheduled_tokens = min(todo, room)
             used += seq.num_scheduled_tokens
+            batch.append(seq)
             if seq.num_cached_tokens + seq.num_scheduled_tokens == seq.num_tokens:
+                self.waiting.popleft()                       # prompt complete after this step
                 seq.status = SequenceStatus.RUNNING
-                self.waiting.popleft()
                 self.running.append(seq)
-            picked.append(seq)
-        return picked
+        return batch
 
-    def _schedule_decode(self) -> list[Sequence]:
-        picked: list[Sequence] = []
-        while self.running and len(picked) < self.max_num_seqs:
+    def _decode_batch(self) -> list[Sequence]:
+        pool = self.block_manager
+        batch: list[Sequence] = []
+        while self.running and len(batch) < self.max_num_seqs:
             seq = self.running.popleft()
-            while not self.block_manager.can_append(seq):
-                if self.running:
-                    self.preempt(self.running.pop())
-                else:
-                    self.preempt(seq)
-                    break
-            else:
-                seq.num_scheduled_tokens = 1
-                seq.is_prefill = False
-                self.block_manager.may_append(seq)
-                picked.append(seq)
-        self.running.extendleft(reversed(picked))
-        return picked
+            while not pool.can_append(seq) and self.running:
+                self.preempt(self.running.pop())             # newest admission gives its pages back
+            if not pool.can_append(seq):
+                self.preempt(seq)
+                continue
+            pool.may_append(seq)
+            seq.num_scheduled_tokens = 1
+            seq.is_prefill = False
+            batch.append(seq)
+        self.running.extendleft(reversed(batch))             # keep the running order
+        return batch
 
     def preempt(self, seq: Sequence) -> None:
+        self.block_manager.deallocate(seq)
         seq.status = SequenceStatus.WAITING
         seq.is_prefill = True
-        self.block_manager.deallocate(seq)
         self.waiting.appendleft(seq)
 
+    # -- after the step --------------------------------------------------------------
     def postprocess(self, seqs: list[Sequence], token_ids: list[int], is_prefill: bool) -> None:
-        for seq, token_id in zip(seqs, token_ids):
-            self.block_manager.hash_blocks(seq)
+        pool = self.block_manager
+        for seq, token in zip(seqs, token_ids):
+            pool.hash_blocks(seq)
             seq.num_cached_tokens += seq.num_scheduled_tokens
             seq.num_scheduled_tokens = 0
             if is_prefill and seq.num_cached_tokens < seq.num_tokens:
-                continue
-            seq.append_token(token_id)
-            hit_eos = not seq.ignore_eos and token_id == self.eos
-            if hit_eos or seq.num_completion_tokens == seq.max_tokens:
+                continue                                     # a chunk of a longer prompt: no token yet
+            seq.append_token(token)
+            if (token == self.eos and not seq.ignore_eos) or seq.num_completion_tokens == seq.max_tokens:
                 seq.status = SequenceStatus.FINISHED
-                self.block_manager.deallocate(seq)
+                pool.deallocate(seq)
                 self.running.remove(seq)
 
     def stats(self) -> dict[str, int]:
-        return {
-            "waiting_sequences": len(self.waiting),
-            "running_sequences": len(self.running),
-            "peak_waiting_sequences": self._peak_waiting,
-            "peak_running_sequences": self._peak_running,
-            "decode_steps_since_prefill": self._decode_steps_since_prefill,
-            "prefill_decode_ratio": self.prefill_decode_ratio,
-            **self.block_manager.stats(),
-        }
+        return {"waiting_sequences": len(self.waiting), "running_sequences": len(self.running),
+                "peak_waiting_sequences": self._peaks["waiting"], "peak_running_sequences": self._peaks["running"],
+                "decode_steps_since_prefill": self._decode_streak, "prefill_decode_ratio": self.prefill_decode_ratio,
+                **self.block_manager.stats()}

@@ -200,3 +200,47 @@ def test_safetensors_checkpoint_round_trip(tmp_path):
     shutil.copy(os.path.join(src, "config.json"), empty / "config.json")
     with pytest.raises(FileNotFoundError, match="no safetensors"):
         LLM(str(empty), max_model_len=2048, num_kvcache_blocks=4)
+
+
+def test_page_pool_prefix_reuse_and_revival():
+    """Full pages are keyed by content: a second prompt with the same prefix maps
+    the first one's pages (shared, ref-counted), a released prefix stays
+    reusable until its pages are handed out again, and the last page is never
+    shared (reference engine/block_manager.py:26-143 behaviour)."""
+    from nanovllm.engine.block_manager import BlockManager
+    from nanovllm.engine.sequence import Sequence
+
+    Sequence.block_size = 4
+    pool = BlockManager(num_blocks=8, block_size=4)
+    a = Sequence(list(range(10)))                       # pages [0-3] [4-7] [8,9]
+    assert pool.can_allocate(a) == 0
+    pool.allocate(a, 0)
+    a.num_scheduled_tokens = 10
+    pool.hash_blocks(a)                                 # keys the two full pages
+    a.num_cached_tokens, a.num_scheduled_tokens = 10, 0
+    b = Sequence(list(range(8)) + [99, 98, 97])         # same two full pages, different tail
+    assert pool.can_allocate(b) == 2
+    pool.allocate(b, 2)
+    assert b.block_table[:2] == a.block_table[:2] and b.block_table[2] != a.block_table[2]
+    assert b.num_cached_tokens == 8 and pool.stats()["allocated_blocks"] == 4
+    a_pages = list(a.block_table)
+    pool.deallocate(a)
+    pool.deallocate(b)
+    assert pool.stats()["allocated_blocks"] == 0 and not a.block_table
+    c = Sequence(list(range(9)))                        # revives the freed, still-keyed prefix pages
+    assert pool.can_allocate(c) == 2
+    pool.allocate(c, 2)
+    assert c.block_table[:2] == a_pages[:2]
+    # a decode step needs a page exactly when the length becomes 1 mod the page size
+    d = Sequence([5] * 4)
+    pool.allocate(d, pool.can_allocate(d))
+    d.append_token(6)
+    assert len(d) % 4 == 1 and pool.can_append(d)
+    before = len(d.block_table)
+    pool.may_append(d)
+    assert len(d.block_table) == before + 1
+    d.append_token(7)
+    pool.may_append(d)
+    assert len(d.block_table) == before + 1
+    s = pool.stats()
+    assert s["prefix_cache_hits"] == 4 and s["freed_blocks"] == 4

@@ -142,3 +142,41 @@ def test_c1_engine_batch1_path_against_golden(tmp_path):
     with open(os.path.join(ROOT, "gpurun_out", "agreement_c1.json"), "w") as f:
         json.dump(report, f, indent=1)
     assert status != "FAIL", details
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_torch_operator_step_matches_ctypes_step(batch):
+    """The step driven through ``torch.ops.nanovllm_megakernel_C.mkd_decode_step``
+    (the C++ shim on the device dispatch key) gives bit-identical tokens, logits
+    and KV writes to the ctypes call of the C ABI, and raises on a bad call."""
+    from nanovllm.backends.megakernel import torch_ops
+    from nanovllm.backends.megakernel.taskgraph import TaskGraphDecoder
+
+    print(f"case: torch operator vs ctypes, batch {batch}", flush=True)
+    h = Harness(num_layers=2, num_blocks=2 * batch + 2, kv_fill_seed=6, variant="tagged")
+    ids = [(311 * (b + 1)) % V for b in range(batch)]
+    pos = [300 + 5 * b for b in range(batch)]
+    tables = [[2 * b + 2, 2 * b + 3] for b in range(batch)]
+    kv0 = h.kv.clone()
+    ref_toks, ref_logits = h.step(ids, pos, tables)
+    kv_ref = h.kv.clone()
+    h.kv.copy_(kv0)
+    op_dec = TaskGraphDecoder(h.w, k_cache=h.kv[0], v_cache=h.kv[1], block_size=256,
+                              num_cache_blocks=2 * batch + 2, max_model_len=2048, binding="torch_ops")
+    h.dec.close()
+    h.dec = op_dec
+    toks, logits = h.step(ids, pos, tables)
+    print(f"  tokens {toks} vs {ref_toks}", flush=True)
+    assert toks == ref_toks
+    assert torch.equal(logits, ref_logits)
+    assert torch.equal(h.kv, kv_ref)
+    # a non-zero return code of the library becomes a RuntimeError with its message
+    ops = torch_ops.load()
+    with pytest.raises(RuntimeError, match="batch must be 1, 2, 4 or 8"):
+        geo = op_dec._geometry(1, 1)
+        inst, num, sched = geo.persistent[0]
+        ops.mkd_decode_step(op_dec._layer_ptrs, h.w["embed"], h.w["final_norm"], h.w["cos"], h.w["sin"],
+                            op_dec._k_cache, op_dec._v_cache, op_dec._table, op_dec._seqlens, op_dec._row_active,
+                            op_dec._ids, op_dec._op_tokens, None, op_dec._workspace, inst, num, sched.grid,
+                            sched.max_inst, 1, 3, 2, 1, 16, 2 * batch + 2, 256)
+    h.close()

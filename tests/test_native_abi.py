@@ -78,3 +78,23 @@ def test_tagged_region_layout_matches_library():
     layout = native.workspace_layout()
     assert layout["end"][0] == lib.mkd_workspace_bytes()
     assert layout["tw_res1"][0] % 256 == 0
+
+
+def test_torch_operator_shim_registers_the_ops():
+    """libmkd_torch_ops.so loads on the CPU and registers the operators with the
+    schema the decoder calls (reference torch_bindings.cpp:227-264 namespace)."""
+    import torch
+
+    if not build.TORCH_OPS_PATH.exists():
+        pytest.skip("libmkd_torch_ops.so not built (run __graft_entry__.build())")
+    from nanovllm.backends.megakernel import torch_ops
+
+    ops = torch_ops.load()
+    schema = str(ops.mkd_decode_step.default._schema)
+    assert schema.startswith("nanovllm_megakernel_C::mkd_decode_step(Tensor layer_ptrs")
+    for arg in ("Tensor(a!) k_cache", "Tensor(e!) workspace", "int block_size"):
+        assert arg in schema, arg
+    assert "Tensor(a!) workspace" in str(ops.mkd_reset_counters.default._schema)
+    # a CPU tensor has no kernel on the CPU key: dispatch fails loudly, no silent fallback
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        ops.mkd_reset_counters(torch.zeros(16, dtype=torch.uint8))
