@@ -121,8 +121,25 @@ def time_decode(dec, batch: int, start_ctx: list[int], steps: int, warmup: int, 
     return elapsed, durs, contexts
 
 
-def cpu_baseline(sample_steps: int = 3):
-    """The CPU oracle (a restatement of the reference torch decode) on this host."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(sample_steps: int = 10):
+    """The CPU oracle (a restatement of the reference torch decode) on this host:
+    `sample_steps` greedy batch-1 steps of the full model, each timed on its own;
+    value = 1 / median step time."""
+
+    import statistics
 
     import torch
     from nanovllm.synthetic import make_weights
@@ -136,33 +153,135 @@ def cpu_baseline(sample_steps: int = 3):
     vc = torch.zeros_like(kc)
     tok = 42
     oracle.decode_step([tok], [0], [[0]], kc, vc)  # warm
-    t0 = time.perf_counter()
+    times = []
     for i in range(sample_steps):
+        t0 = time.perf_counter()
         _, toks = oracle.decode_step([tok], [i + 1], [[0]], kc, vc)
+        times.append(time.perf_counter() - t0)
         tok = toks[0]
-    dt = time.perf_counter() - t0
-    return {"value": sample_steps / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{sample_steps} greedy decode steps, batch 1, ctx 2..{sample_steps + 1}, full 28-layer "
-                      f"model, torch CPU fp32-accumulate restatement (oracle/qwen3_oracle.py)"}
+    med = statistics.median(times)
+    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_model": cpu_model(),
+            "step_s": {"median": round(med, 4), "min": round(min(times), 4), "max": round(max(times), 4),
+                       "stdev": round(statistics.stdev(times), 4), "n": sample_steps},
+            "sample": f"{sample_steps} greedy decode steps (each timed), batch 1, ctx 2..{sample_steps + 1}, full "
+                      f"28-layer model, torch CPU fp32-accumulate restatement (oracle/qwen3_oracle.py); "
+                      f"value = 1 / median step time"}
 
 
 PERSISTENT_KERNELS = {"lds_dma": "k_persistent2", "v1": "k_persistent",
                       "tagged": "k_persistent4"}
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_c3.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+CSRC = os.path.join(ROOT, "decode-fusion-boundary_amd", "csrc")
+
+
+def kernel_source_hash() -> str:
+    """sha256 over the HIP sources of the decode library: a PMC summary is only
+    used for the kernels it was measured on."""
+
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(CSRC)):
+        if name.endswith((".h", ".hip")):
+            with open(os.path.join(CSRC, name), "rb") as f:
+                h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
 
 
 def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
-    (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel's reading), or None."""
+    """HBM bytes per launch of `kernel` (e.g. ``k_persistent4<1>``) from the
+    committed rocprofv3 PMC summary (``bench.py --pmc-collect``: FETCH_SIZE and
+    WRITE_SIZE per dispatch, scaled by a copy kernel's readings). Returns
+    (bytes or None, note)."""
 
     try:
         with open(TRAFFIC_FILE) as f:
-            for line in f:
-                if line.startswith("traffic_bytes_per_launch") and kernel in line:
-                    return int(line.split("=")[1].split()[0])
-    except OSError:
-        return None
-    return None
+            pmc = json.load(f)
+    except (OSError, ValueError):
+        return None, "no PMC summary"
+    if pmc.get("source_hash") != kernel_source_hash():
+        return None, "PMC summary measured on other kernel sources (stale); rerun bench.py --pmc-collect"
+    entry = pmc.get("kernels", {}).get(kernel)
+    if entry is None:
+        return None, f"no PMC entry for {kernel}"
+    return int(entry["traffic_bytes"]), f"{TRAFFIC_FILE.split(ROOT + os.sep)[-1]} (source {pmc['source_hash']})"
+
+
+def _pmc_run(counter: str, args: list[str], out_dir: str) -> dict:
+    """One rocprofv3 counter pass over a child bench process; returns
+    {kernel name: mean counter value per dispatch}."""
+
+    import csv
+    import glob
+    import shutil
+    import subprocess
+
+    shutil.rmtree(out_dir, ignore_errors=True)
+    cmd = ["timeout", "-s", "KILL", "240", "rocprofv3", "--pmc", counter, "-d", out_dir, "-o", "pmc",
+           "--output-format", "csv", "--", sys.executable, os.path.abspath(__file__), *args]
+    print("pmc:", " ".join(cmd), file=sys.stderr, flush=True)
+    subprocess.run(cmd, check=True, cwd=ROOT, stdout=subprocess.DEVNULL)
+    per_dispatch: dict[tuple[str, str], float] = {}
+    for path in glob.glob(os.path.join(out_dir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                key = (row["Kernel_Name"], row.get("Dispatch_Id", ""))
+                per_dispatch[key] = per_dispatch.get(key, 0.0) + float(row["Counter_Value"])
+    out: dict[str, list[float]] = {}
+    for (kernel, _), v in per_dispatch.items():
+        out.setdefault(kernel, []).append(v)
+    return {k: sum(v) / len(v) for k, v in out.items()}
+
+
+def pmc_collect(out_path: str) -> dict:
+    """Measure HBM traffic per launch of the persistent kernel at batch 1, 2, 4, 8
+    (C3 shape, context 1..9) with rocprofv3 FETCH_SIZE and WRITE_SIZE, each in a
+    pass of its own, calibrated by a 1 GiB device copy; writes the summary JSON."""
+
+    import re
+
+    kargs = ["--only-kernel", "--no-sweep", "--no-cpu-baseline", "--steps", "8", "--warmup", "2",
+             "--pmc-batches", "1,2,4,8"]
+    base = os.path.join(ROOT, "gpurun_out", "pmc")
+    fetch = _pmc_run("FETCH_SIZE", kargs, os.path.join(base, "fetch"))
+    write = _pmc_run("WRITE_SIZE", kargs, os.path.join(base, "write"))
+    cfetch = _pmc_run("FETCH_SIZE", ["--copy-calibration"], os.path.join(base, "fetch_copy"))
+    cwrite = _pmc_run("WRITE_SIZE", ["--copy-calibration"], os.path.join(base, "write_copy"))
+    copy_kib = (1 << 30) / 1024
+    f_copy = max(v for k, v in cfetch.items() if "copy" in k.lower())
+    w_copy = max(v for k, v in cwrite.items() if "copy" in k.lower())
+    fetch_factor, write_factor = copy_kib / f_copy, copy_kib / w_copy
+    kernels = {}
+    for name, fk in fetch.items():
+        m = re.search(r"(k_persistent\d?)<(\d)>", name)
+        if not m:
+            continue
+        key = f"{m.group(1)}<{m.group(2)}>"
+        wk = next((v for n, v in write.items() if key in n.replace(" ", "")), None)
+        if wk is None:
+            continue
+        b = int(m.group(2))
+        algorithmic = sum(step_bytes([c] * b) for c in range(1, 9)) / 8
+        traffic = fk * 1024 * fetch_factor + wk * 1024 * write_factor
+        kernels[key] = {"fetch_kib": round(fk, 2), "write_kib": round(wk, 2),
+                        "read_bytes": int(fk * 1024 * fetch_factor), "written_bytes": int(wk * 1024 * write_factor),
+                        "traffic_bytes": int(traffic), "algorithmic_bytes": int(algorithmic),
+                        "traffic_over_algorithmic": round(traffic / algorithmic, 4)}
+    summary = {"source_hash": kernel_source_hash(),
+               "workload": "C3 shape: batch B, contexts 1..9 (8 timed steps after 2 warmup), tagged persistent kernel",
+               "calibration": {"copy_bytes_each_way": 1 << 30, "fetch_kib_per_copy": round(f_copy, 2),
+                               "write_kib_per_copy": round(w_copy, 2), "fetch_factor": round(fetch_factor, 4),
+                               "write_factor": round(write_factor, 4)},
+               "commands": [f"rocprofv3 --pmc {c} -d <dir> -o pmc --output-format csv -- python3 bench.py "
+                            + " ".join(a) for c in ("FETCH_SIZE", "WRITE_SIZE")
+                            for a in (kargs, ["--copy-calibration"])],
+               "kernels": kernels}
+    with open(out_path, "w") as f:
+        json.dump(summary, f, indent=1)
+    return summary
 
 
 def copy_calibration(nbytes: int = 1 << 30, launches: int = 4):
@@ -293,12 +412,22 @@ def main():
                     help="LLM.generate end to end, megakernel vs torch decode backend (C4 shape)")
     ap.add_argument("--fusion-sweep", action="store_true",
                     help="persistent kernel at fusion_groups 1/2/4/7/14/28, batch 1 and 8")
+    ap.add_argument("--pmc-collect", action="store_true",
+                    help="rocprofv3 FETCH_SIZE/WRITE_SIZE passes (child processes) -> gpurun_out/pmc_traffic.json")
+    ap.add_argument("--pmc-batches", default="",
+                    help="with --only-kernel: run the timed loop at each of these batch sizes (PMC passes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode step runs TP=1 on a single MI355X; "
               "multi-GPU data parallelism is independent replicas of this step. Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+    if args.pmc_collect:
+        # (children do the GPU work; this process never touches the device)
+        out = os.path.join(ROOT, "gpurun_out", "pmc_traffic.json")
+        os.makedirs(os.path.dirname(out), exist_ok=True)
+        print(json.dumps(pmc_collect(out)))
+        return
     import torch
 
     if not torch.cuda.is_available():
@@ -324,6 +453,12 @@ def main():
         print(json.dumps(res))
         return
     _, _, _, dec = build_decoder(num_blocks=8 * 8 + 8, variant=args.variant, attn_splits=args.attn_splits)
+    if args.only_kernel and args.pmc_batches:
+        for b in (int(x) for x in args.pmc_batches.split(",")):
+            el, _, _ = time_decode(dec, b, [args.start_ctx] * b, args.steps, args.warmup, args.mode)
+            print(json.dumps({"batch": b, "ms_per_step": el * 1e3 / args.steps}), flush=True)
+        dec.close()
+        return
     start = [args.start_ctx] * args.batch
     elapsed, durs, contexts = time_decode(dec, args.batch, start, args.steps, args.warmup, args.mode,
                                           per_launch_events=True)
@@ -336,10 +471,10 @@ def main():
     achieved = bytes_per_launch / (avg_launch_ms * 1e-3) / 1e9
     if args.mode == "persistent":
         kernel = f"{PERSISTENT_KERNELS[args.variant]}<{args.batch}> (one launch per decode step)"
-        traffic = measured_traffic(f"{PERSISTENT_KERNELS[args.variant]}<{args.batch}>")
+        traffic, traffic_src = measured_traffic(f"{PERSISTENT_KERNELS[args.variant]}<{args.batch}>")
     else:
         kernel = f"all stage kernels of one step ({args.mode})"
-        traffic = None
+        traffic, traffic_src = None, "per-op path: no single dominant kernel"
     result = {
         "metric": "device us/decode-step & tok/s at batch 1-8 vs 1.19GB HBM weight floor",
         "value": round(args.batch * args.steps / elapsed, 2),
@@ -362,7 +497,7 @@ def main():
                    "seq_len": args.steps, "parallelism": "single GPU (tp1)", "launch": args.mode},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": kernel,
+                     "traffic_source": traffic_src, "kernel": kernel,
                      "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_ms * 1e3, 2)},
     }
     if not args.no_sweep:

@@ -8,8 +8,10 @@
 // (csrc/torch_bindings.cpp:65-184 tg_decode_step, :186-225 tg_zero_regions,
 // :227-264 TORCH_LIBRARY registration): same namespace, operators registered on
 // the device dispatch key (ROCm's HIP device is torch's "CUDA" key).
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+// PyTorch-ROCm keeps its HIP devices under torch's "cuda" device type; the
+// guard and stream of that arrangement are the *MasqueradingAsCUDA ones.
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
 
 #include <optional>
@@ -97,8 +99,8 @@ void mkd_decode_step(const at::Tensor& layer_ptrs, const at::Tensor& embed, cons
   d.lm_slots = (int32_t)lm_slots;
   d.flags = (uint32_t)flags;
   MkdSchedule s{inst.data_ptr<int32_t>(), num_inst.data_ptr<int32_t>(), (int32_t)grid, (int32_t)max_inst};
-  c10::hip::HIPGuard guard(dev);
-  check_rc(mkd_launch_persistent(&d, &s, c10::hip::getCurrentHIPStream(dev.index()).stream()),
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
+  check_rc(mkd_launch_persistent(&d, &s, c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(dev.index()).stream()),
            "mkd_launch_persistent");
 }
 
@@ -110,8 +112,8 @@ void mkd_reset(const at::Tensor& workspace) {
   MkdStepDesc d{};
   d.workspace = workspace.data_ptr();
   d.workspace_bytes = (uint64_t)workspace.numel();
-  c10::hip::HIPGuard guard(workspace.device());
-  check_rc(mkd_reset_counters(&d, c10::hip::getCurrentHIPStream(workspace.device().index()).stream()),
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(workspace.device());
+  check_rc(mkd_reset_counters(&d, c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(workspace.device().index()).stream()),
            "mkd_reset_counters");
 }
 
