@@ -395,6 +395,9 @@ int mkd_graph_create(const MkdStepDesc* d, int32_t mode, const MkdSchedule* s, c
                      const MkdStage* stages, int32_t num_stages, int32_t steps, void* stream, void** out) {
   if (out == nullptr) return fail(MKD_E_INVALID, "null graph handle");
   if (steps < 1) return fail(MKD_E_INVALID, "steps must be >= 1");
+  if (mode < 0 || mode > 2) return fail(MKD_E_INVALID, "graph mode must be 0, 1 or 2");
+  if (mode == 2 && (s == nullptr || num_stages < 1))
+    return fail(MKD_E_INVALID, "mode 2 needs an array of num_stages >= 1 persistent schedules");
   int rc = validate(d);
   if (rc) return rc;
   hipStream_t cap = nullptr;
@@ -406,8 +409,14 @@ int mkd_graph_create(const MkdStepDesc* d, int32_t mode, const MkdSchedule* s, c
     hipStreamDestroy(cap);
     return hip_fail(e, "hipStreamBeginCapture");
   }
-  for (int i = 0; i < steps && rc == MKD_OK; i++)
-    rc = mode == 1 ? do_persistent(d, s, cap) : do_stages(d, inst, stages, num_stages, cap);
+  for (int i = 0; i < steps && rc == MKD_OK; i++) {
+    if (mode == 2) {
+      // one persistent launch per schedule of the array, in order
+      for (int k = 0; k < num_stages && rc == MKD_OK; k++) rc = do_persistent(d, s + k, cap);
+    } else {
+      rc = mode == 1 ? do_persistent(d, s, cap) : do_stages(d, inst, stages, num_stages, cap);
+    }
+  }
   e = hipStreamEndCapture(cap, &g->graph);
   if (rc == MKD_OK && e != hipSuccess) rc = hip_fail(e, "hipStreamEndCapture");
   if (rc == MKD_OK) {

@@ -303,8 +303,12 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
 // only by the first RMSNorm task of a launch (valid still false).
 // Gate/up task word a2 flag (tagged kernel): publish the residual, read by
 // the next layer's QKV prologue in the next launch (the last layer of a layer
-// segment that is not the step's last).
+// segment that is not the step's last, and every layer when each stage is a
+// launch of its own).
 constexpr int GATEUP_PUBLISH_RES = 1;
+// QKV task word a2 flag: publish the residual after the input add, read by the
+// same layer's gate/up prologue in a later launch (one launch per stage).
+constexpr int QKV_PUBLISH_RES = 1;
 template <int B>
 struct ResKeep {
   uint32_t w[B][2];
@@ -684,11 +688,13 @@ __device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, c
   const int t = p4_tid();
   switch (w.op) {
     // (the residual after QKV is consumed by the gate/up prologue of the same
-    // layer, always in the same launch: never published)
+    // layer: published only when that prologue runs in a later launch)
     case MKD_OP_QKV: {
       const uint16_t* nw = p4_wptr(d, layer, MKD_W_LN_IN);
-      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, 0, 0, rk);
-      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, 0, 0, rk);
+      const ResRange r = p4_res_range<QKV_N / 256>(w);
+      const int rn = (w.a2 & QKV_PUBLISH_RES) ? r.n : 0;
+      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, r.first, rn, rk);
+      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, r.first, rn, rk);
     }
     case MKD_OP_GATEUP: {
       const ResRange r = p4_res_range<I / 256>(w);
@@ -904,6 +910,7 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
   uint8_t* const twb = reinterpret_cast<uint8_t*>(c.ws.tw(BASE + (uint32_t)(w.a0 >> 1)));
   ResWord rw{nullptr, 0};
   if (OP == MKD_OP_GATEUP && (w.a2 & GATEUP_PUBLISH_RES)) rw = p4_residual_word<B, I / 256>(c, w, TW_RES2, tag);
+  if (OP == MKD_OP_QKV && (w.a2 & QKV_PUBLISH_RES)) rw = p4_residual_word<B, QKV_N / 256>(c, w, TW_RES1, tag);
   for (int e = fo; e < n; e += PK_CW * 64) {
     const int r = e & ((1 << LR) - 1), b = (e >> LR) & (B - 1), i = e >> (LR + LB);
     float v0, v1;

@@ -27,6 +27,8 @@ ATTN_QHEAD = 64
 ATTN_ONE_HEAD = 128
 # GATEUP task word a2 (tagged kernel): publish the residual for the next launch
 GATEUP_PUBLISH_RES = 1
+# QKV task word a2 (tagged kernel, one launch per stage): publish the residual after the input add
+QKV_PUBLISH_RES = 1
 
 FLAG_ADVANCE = 1
 FLAG_ZERO_FANIN = 2

@@ -30,7 +30,7 @@ import dataclasses
 from dataclasses import dataclass, field
 
 from .native import (
-    ATTN_ONE_HEAD, ATTN_QHEAD, GATEUP_PUBLISH_RES, INST_WORDS, MAX_BATCH, MAX_LM_SLOTS, MAX_SPLITS, OP_ATTN, OP_DOWN, OP_GATEUP,
+    ATTN_ONE_HEAD, ATTN_QHEAD, GATEUP_PUBLISH_RES, QKV_PUBLISH_RES, INST_WORDS, MAX_BATCH, MAX_LM_SLOTS, MAX_SPLITS, OP_ATTN, OP_DOWN, OP_GATEUP,
     OP_LMHEAD, OP_OPROJ, OP_QKV,
 )
 
@@ -344,4 +344,27 @@ def build_segments(batch: int, attn_splits: int, num_wgs: int, num_layers: int =
                    if s.op == OP_GATEUP and s.layer == end - 1 else s for s in seg]
         out.append(Schedule(batch=batch, attn_splits=attn_splits, num_layers=num_layers,
                             grid=num_wgs, stages=seg, rows=place_xcd_aware(seg, num_wgs)))
+    return out
+
+
+def build_stage_schedules(batch: int, attn_splits: int, num_layers: int = NUM_LAYERS,
+                          max_grid: int = 256) -> list[Schedule]:
+    """The per-op comparator on the tagged persistent kernel's own task bodies:
+    one persistent launch per stage, one task per workgroup (``grid`` = the
+    stage's task count). Every QKV task publishes the residual after the input
+    add and every gate/up task the residual after the post-attention add, since
+    each consumer runs in a later launch and cannot keep them in registers. A
+    stage's workgroups must all be resident (the last split-KV task and the last
+    LM slot wait on their stage siblings), so a stage holds at most ``max_grid``
+    tasks."""
+
+    out = []
+    for st in build_stages(batch, attn_splits, max_grid, num_layers, q_head_tasks=True):
+        flag = QKV_PUBLISH_RES if st.op == OP_QKV else (GATEUP_PUBLISH_RES if st.op == OP_GATEUP else 0)
+        tasks = [dataclasses.replace(t, a2=t.a2 | flag) for t in st.tasks] if flag else list(st.tasks)
+        if len(tasks) > max_grid:
+            raise ValueError(f"stage {st.op} of layer {st.layer} has {len(tasks)} tasks; one launch holds "
+                             f"at most {max_grid} co-resident workgroups (reduce the split-KV factor)")
+        out.append(Schedule(batch=batch, attn_splits=attn_splits, num_layers=num_layers, grid=len(tasks),
+                            stages=[Stage(st.op, st.layer, tasks)], rows=[[t] for t in tasks]))
     return out

@@ -22,6 +22,7 @@ device error word and the sampled tokens.
 
 from __future__ import annotations
 
+import dataclasses
 import os
 from dataclasses import dataclass
 from typing import Any
@@ -33,7 +34,7 @@ from nanovllm.model_spec import QWEN3_06B
 from . import native
 from .row_contract import row_active_mask
 from .schedule import (
-    NUM_LAYERS, Schedule, auto_attn_splits, batch_bucket, build_schedule, build_segments,
+    NUM_LAYERS, Schedule, auto_attn_splits, batch_bucket, build_schedule, build_segments, build_stage_schedules,
 )
 from .verifier import verify
 from .weights import pack_layer_pointers
@@ -133,6 +134,10 @@ class _Geometry:
     stages: Any            # ctypes array of MkdStage
     num_stages: int
     graph: Any = None      # captured per-op hipGraph (launch="graph")
+    # tagged variant: the per-op comparator on the persistent kernel's task bodies,
+    # one persistent launch per stage ((inst, num, MkdSchedule) each, and the array)
+    stage_persistent: list = dataclasses.field(default_factory=list)
+    stage_array: Any = None
 
 
 def _check_tagged_preconditions(segs) -> None:
@@ -313,6 +318,19 @@ class TaskGraphDecoder:
         stages = (native.MkdStage * len(table))(*[native.MkdStage(*row) for row in table])
         geo = _Geometry(batch=batch, attn_splits=splits, segments=segs, persistent=persistent,
                         stage_inst=stage_inst, stages=stages, num_stages=len(table))
+        try:
+            stage_scheds = build_stage_schedules(batch, splits, self.num_layers, max_grid=self.grid) if tagged else []
+        except ValueError:
+            stage_scheds = []   # a stage too large to be co-resident: the generic per-op kernels serve it
+        if stage_scheds:
+            for sch in stage_scheds:
+                flat, counts = sch.persistent_words()
+                inst = torch.tensor(flat, dtype=torch.int32).to(self.device)
+                num = torch.tensor(counts, dtype=torch.int32).to(self.device)
+                geo.stage_persistent.append((inst, num, native.MkdSchedule(
+                    inst=inst.data_ptr(), num_inst=num.data_ptr(), grid=sch.grid, max_inst=sch.max_inst)))
+            arr = (native.MkdSchedule * len(geo.stage_persistent))(*[x[2] for x in geo.stage_persistent])
+            geo.stage_array = arr
         self._geometries[key] = geo
         return geo
 
@@ -371,18 +389,35 @@ class TaskGraphDecoder:
                     torch.cuda.current_stream(self.device).synchronize()
                     on_segment(i, geo.segments[i])
         elif mode == "stages":
-            native.check(self._lib.mkd_launch_stages(native.ctypes.byref(desc), geo.stage_inst.data_ptr(),
-                                                     geo.stages, geo.num_stages, stream))
+            if geo.stage_array is not None:   # tagged: one persistent launch per stage
+                for _, _, sched in geo.stage_persistent:
+                    native.check(self._lib.mkd_launch_persistent(native.ctypes.byref(desc),
+                                                                 native.ctypes.byref(sched), stream))
+            else:
+                native.check(self._lib.mkd_launch_stages(native.ctypes.byref(desc), geo.stage_inst.data_ptr(),
+                                                         geo.stages, geo.num_stages, stream))
         else:  # graph
             if geo.graph is None or geo.graph[0] != (desc.rows, desc.flags, desc.out_logits):
                 if geo.graph is not None:
                     self._lib.mkd_graph_destroy(geo.graph[1])
-                handle = native.ctypes.c_void_p()
-                native.check(self._lib.mkd_graph_create(
-                    native.ctypes.byref(desc), 0, None, geo.stage_inst.data_ptr(), geo.stages,
-                    geo.num_stages, 1, stream, native.ctypes.byref(handle)))
-                geo.graph = ((desc.rows, desc.flags, desc.out_logits), handle)
+                geo.graph = ((desc.rows, desc.flags, desc.out_logits), self._capture(desc, geo, stream))
             native.check(self._lib.mkd_graph_launch(geo.graph[1], stream))
+
+    def _capture(self, desc: native.MkdStepDesc, geo: _Geometry, stream: int):
+        """hipGraph of one step's per-op launches: for the tagged variant the
+        persistent kernel once per stage (mode 2), otherwise the generic stage
+        kernels (mode 0)."""
+
+        handle = native.ctypes.c_void_p()
+        if geo.stage_array is not None:
+            native.check(self._lib.mkd_graph_create(
+                native.ctypes.byref(desc), 2, geo.stage_array, None, None, len(geo.stage_persistent), 1, stream,
+                native.ctypes.byref(handle)))
+        else:
+            native.check(self._lib.mkd_graph_create(
+                native.ctypes.byref(desc), 0, None, geo.stage_inst.data_ptr(), geo.stages, geo.num_stages, 1,
+                stream, native.ctypes.byref(handle)))
+        return handle
 
     def _launch_op(self, desc: native.MkdStepDesc, inst, num, sched: native.MkdSchedule) -> None:
         """One persistent launch through the registered torch operator (same
@@ -411,13 +446,18 @@ class TaskGraphDecoder:
         return status[16:16 + rows].tolist()
 
     def splits_for(self, max_context: int, batch: int = 1, mode: str | None = None) -> int:
-        """Split-KV factor for a step. The tagged persistent kernel caps splits at
-        16 // batch bucket; the per-op stage kernels need many workgroups per launch
-        and keep one split per 256 positions (measured at C5, batch 8: 2358 us per step
-        with 8 splits, 2692 us with 2)."""
+        """Split-KV factor for a step. The tagged kernel (persistent, and its per-op
+        launches) caps splits at 16 // batch bucket; the generic per-op stage kernels
+        (lds_dma variant) need many workgroups per launch and keep one split per 256
+        positions (measured at C5, batch 8: 2358 us per step with 8 splits, 2692 us
+        with 2)."""
 
-        capped = (mode or self.launch) == "persistent" and self.persistent_variant == "tagged"
-        return auto_attn_splits(max_context, self.min_attn_splits, batch_bucket(batch) if capped else 1)
+        if self.persistent_variant == "tagged":
+            # both launch modes run the tagged kernel: at most 16 // batch splits (a
+            # per-stage launch holds every attention task of the stage co-resident)
+            cap = native.MAX_SPLITS // batch_bucket(batch)
+            return min(auto_attn_splits(max_context, self.min_attn_splits, batch_bucket(batch)), cap)
+        return auto_attn_splits(max_context, self.min_attn_splits, 1)
 
     # -- decode ----------------------------------------------------------------
     def decode_rows(self, input_ids, positions, block_tables, active_rows=None, logits=None,
@@ -541,10 +581,7 @@ class TaskGraphDecoder:
         geo = self._geometry(batch_bucket(rows), self.splits_for(max_context, rows, mode))
         desc = self._desc_for(rows, geo, flags=native.FLAG_ADVANCE)
         if mode == "graph":
-            handle = native.ctypes.c_void_p()
-            native.check(self._lib.mkd_graph_create(
-                native.ctypes.byref(desc), 0, None, geo.stage_inst.data_ptr(), geo.stages,
-                geo.num_stages, 1, self._stream_ptr(), native.ctypes.byref(handle)))
+            handle = self._capture(desc, geo, self._stream_ptr())
             self._owned_graphs = getattr(self, "_owned_graphs", []) + [handle]
             return lambda: native.check(self._lib.mkd_graph_launch(handle, self._stream_ptr()))
         return lambda: self._launch(desc, geo, mode)

@@ -182,9 +182,13 @@ int mkd_check_error(const MkdStepDesc* desc, void* stream, int32_t* code);
 int mkd_launch_persistent_noalloc(const MkdStepDesc* desc, const MkdSchedule* sched, int32_t* status,
                                   void* stream);
 
-/* Captured hipGraph of either launch mode ("graph" comparator / replay path).
- * mode 0 = per-op stages, 1 = persistent. `steps` consecutive decode steps are
- * captured (use MKD_FLAG_ADVANCE to feed each step's token to the next). */
+/* Captured hipGraph of a launch mode ("graph" comparator / replay path).
+ * mode 0 = per-op stages of the generic task kernels (inst/stages/num_stages),
+ * 1 = one persistent launch (sched), 2 = one persistent launch per schedule of
+ * the array sched[0 .. num_stages-1] (the per-op comparator on the persistent
+ * kernel's own task bodies: one stage per schedule, one task per workgroup).
+ * `steps` consecutive decode steps are captured (use MKD_FLAG_ADVANCE to feed
+ * each step's token to the next). */
 int mkd_graph_create(const MkdStepDesc* desc, int32_t mode, const MkdSchedule* sched,
                      const int32_t* inst, const MkdStage* stages, int32_t num_stages,
                      int32_t steps, void* stream, void** graph_out);

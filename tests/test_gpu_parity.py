@@ -29,7 +29,8 @@ LOGIT_TOL = 2e-2
 MODES = ["persistent", "stages", "graph"]
 VARIANTS = ["lds_dma", "tagged"]   # persistent-kernel variants
 # (launch mode, persistent variant) pairs: every launch path once
-PATHS = [("persistent", "lds_dma"), ("persistent", "tagged"), ("stages", "lds_dma"), ("graph", "lds_dma")]
+PATHS = [("persistent", "lds_dma"), ("persistent", "tagged"), ("stages", "lds_dma"), ("graph", "lds_dma"),
+         ("stages", "tagged"), ("graph", "tagged")]
 
 
 def check_tokens(toks, ref_toks, ref_logits, bound):
@@ -215,7 +216,8 @@ def test_inactive_row_leaves_its_pages_untouched(variant):
     h.close()
 
 
-@pytest.mark.parametrize("mode,variant", [("persistent", "lds_dma"), ("persistent", "tagged"), ("graph", "lds_dma")])
+@pytest.mark.parametrize("mode,variant", [("persistent", "lds_dma"), ("persistent", "tagged"), ("graph", "lds_dma"),
+                                          ("graph", "tagged")])
 def test_split_kv_long_ragged_context(mode, variant):
     """Ragged contexts up to ~1.8k positions: split-KV (auto splits) + LSE merge,
     against the oracle with the torch-relative bound (long random-KV attention
@@ -240,7 +242,7 @@ def test_split_kv_long_ragged_context(mode, variant):
     h.close()
 
 
-@pytest.mark.parametrize("mode,variant", [("persistent", "tagged"), ("graph", "lds_dma")])
+@pytest.mark.parametrize("mode,variant", [("persistent", "tagged"), ("graph", "lds_dma"), ("graph", "tagged")])
 def test_batch8_long_ragged_context(mode, variant):
     """Eight rows with ragged contexts up to 2000 on scattered pages. The tagged
     kernel runs 2 splits here (batch-capped, ~1000 positions per split), and the
@@ -309,7 +311,8 @@ def test_greedy_decode_sixteen_steps_matches_oracle(variant):
     h.close()
 
 
-@pytest.mark.parametrize("mode,variant", [("persistent", "lds_dma"), ("persistent", "tagged"), ("graph", "lds_dma")])
+@pytest.mark.parametrize("mode,variant", [("persistent", "lds_dma"), ("persistent", "tagged"), ("graph", "lds_dma"),
+                                          ("graph", "tagged")])
 def test_device_resident_steps_match_host_steps(mode, variant):
     """The benchmark's device-resident loop (token fed back and position advanced
     by the step itself, no host sync between steps) produces the same tokens as
@@ -334,4 +337,28 @@ def test_device_resident_steps_match_host_steps(mode, variant):
         cur = toks
     print(f"  device {seq_dev}\n  oracle {seq_ref}", flush=True)
     assert seq_dev == seq_ref
+    h.close()
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_per_stage_launches_match_persistent_bitwise(batch):
+    """The per-op comparator of the tagged variant runs the persistent kernel's
+    own task bodies, one launch per stage: same arithmetic in the same order, so
+    its logits, tokens and KV writes equal the single persistent launch's bit
+    for bit (4 layers, ragged contexts with 2 or 1 splits)."""
+    print(f"case: per-stage launches vs one persistent launch, batch {batch}", flush=True)
+    h = Harness(num_layers=4, num_blocks=3 * batch + 2, kv_fill_seed=8, variant="tagged")
+    ids = [(1299709 * (b + 1)) % 151936 for b in range(batch)]
+    pos = [(317 * (b + 1)) % 700 for b in range(batch)]
+    tables = [[3 * b + 2, 3 * b + 3, 3 * b + 4][:p // 256 + 1] for b, p in enumerate(pos)]
+    kv0 = h.kv.clone()
+    out = {}
+    for mode in ("persistent", "stages", "graph"):
+        h.kv.copy_(kv0)
+        toks, logits = h.step(ids, pos, tables, mode=mode)
+        out[mode] = (toks, logits, h.kv.clone())
+    for mode in ("stages", "graph"):
+        assert out[mode][0] == out["persistent"][0], mode
+        assert torch.equal(out[mode][1], out["persistent"][1]), mode
+        assert torch.equal(out[mode][2], out["persistent"][2]), mode
     h.close()

@@ -180,3 +180,30 @@ def test_xcd_aware_placement_keeps_heads_on_their_die():
                 if t.op in (native.OP_QKV, native.OP_ATTN):
                     assert task_kv_head(t) % 8 == w % 8
             assert sum(t.op == native.OP_LMHEAD for t in row) == 1
+
+
+def test_stage_schedules_one_task_per_workgroup_with_published_residuals():
+    """The per-op comparator on the tagged kernel: one launch per stage, one task
+    per workgroup, every QKV and gate/up task publishing its residual, stages in
+    the persistent schedule's order, and no stage larger than the grid."""
+    from nanovllm.backends.megakernel import native
+    from nanovllm.backends.megakernel.schedule import build_stage_schedules, build_stages
+
+    for batch, splits in ((1, 1), (1, 16), (8, 2), (4, 4)):
+        scheds = build_stage_schedules(batch, splits, num_layers=3, max_grid=256)
+        ref = build_stages(batch, splits, 256, 3, q_head_tasks=True)
+        assert [(s.stages[0].op, s.stages[0].layer) for s in scheds] == [(s.op, s.layer) for s in ref]
+        for s, r in zip(scheds, ref):
+            assert s.grid == len(r.tasks) <= 256 and all(len(row) == 1 for row in s.rows)
+            for t, u in zip((row[0] for row in s.rows), r.tasks):
+                if t.op == native.OP_QKV:
+                    assert t.a2 & native.QKV_PUBLISH_RES
+                elif t.op == native.OP_GATEUP:
+                    assert t.a2 & native.GATEUP_PUBLISH_RES
+                else:
+                    assert t == u
+        assert scheds[-1].stages[0].op == native.OP_LMHEAD and scheds[-1].grid == 256
+    import pytest
+
+    with pytest.raises(ValueError, match="co-resident"):
+        build_stage_schedules(8, 4, num_layers=1, max_grid=256)   # 8 x 16 x 4 = 512 attention tasks
