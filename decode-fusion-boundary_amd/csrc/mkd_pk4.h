@@ -1165,7 +1165,10 @@ __device__ __forceinline__ void p4_fold_splits(const Ws ws, size_t pbase, int ns
     }
   }
 }
-constexpr int ATTN_QHEAD = 64, ATTN_ONE_HEAD = 128;  // task word a0 flags (b * 8 + h < 64)
+constexpr int ATTN_QHEAD = 64, ATTN_ONE_HEAD = 128;
+#ifndef MKD_B1_FOLD_SPR
+#define MKD_B1_FOLD_SPR 3
+#endif  // task word a0 flags (b * 8 + h < 64)
 template <int B, int NS>
 __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int a0, int split, int nsplit,
                                         uint64_t* tr, uint8_t* ring, int cc, int& nch) {
@@ -1356,26 +1359,32 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     return true;
   }
   if constexpr (B == 1) {
-    // batch 1: the last split folds the other splits' partials here, one split
-    // per round (both thread halves alike: dividing the splits between them,
-    // like batch 8, measured 4 % faster at ctx 1500 but slowed the
-    // short-context step by 1 %)
-    for (int sp = 0; nsplit > 1 && sp < nsplit - 1; sp++) {
-      const size_t ps = pbase + (size_t)sp * PART_STRIDE;
-      uint64_t e[3];
-      ok = ok && poll_tagged<3>(
+    // batch 1: the last split folds the other splits' partials here, up to
+    // SPR splits per poll round (all of a round's loads in flight at once:
+    // one round trip instead of one per split), in split order
+    constexpr int SPR = MKD_B1_FOLD_SPR;
+    for (int sp0 = 0; nsplit > 1 && sp0 < nsplit - 1; sp0 += SPR) {
+      uint64_t e[3 * SPR];
+      // (entries past the last split repeat its words)
+      ok = ok && poll_tagged<3 * SPR>(
                      [&](int k) {
-                       return c.ws.tw(ps + (k == 0 ? (size_t)(g * HD + dd) : (size_t)(GROUP * HD + (k - 1) * GROUP + g)));
+                       const int sp = min(sp0 + k / 3, nsplit - 2), f = k % 3;
+                       const size_t ps = pbase + (size_t)sp * PART_STRIDE;
+                       return c.ws.tw(ps + (f == 0 ? (size_t)(g * HD + dd) : (size_t)(GROUP * HD + (f - 1) * GROUP + g)));
                      },
                      e, tag, c.ws);
-      const float ns = __uint_as_float((uint32_t)e[0]), ms = __uint_as_float((uint32_t)e[1]);
-      const float ls = __uint_as_float((uint32_t)e[2]);
-      if (ms == -INFINITY) continue;
-      const float nm = fmaxf(M, ms);
-      const float sa = M == -INFINITY ? 0.f : ex2(M - nm), sb = ex2(ms - nm);
-      num = num * sa + ns * sb;
-      den = den * sa + ls * sb;
-      M = nm;
+#pragma unroll
+      for (int q = 0; q < SPR; q++) {
+        if (sp0 + q >= nsplit - 1) break;
+        const float ns = __uint_as_float((uint32_t)e[3 * q]), ms = __uint_as_float((uint32_t)e[3 * q + 1]);
+        const float ls = __uint_as_float((uint32_t)e[3 * q + 2]);
+        if (ms == -INFINITY) continue;
+        const float nm = fmaxf(M, ms);
+        const float sa = M == -INFINITY ? 0.f : ex2(M - nm), sb = ex2(ms - nm);
+        num = num * sa + ns * sb;
+        den = den * sa + ls * sb;
+        M = nm;
+      }
     }
   }
   if constexpr (B == 8) {

@@ -75,6 +75,35 @@ def batch_bucket(rows: int) -> int:
     raise ValueError(f"batch {rows} exceeds the compiled maximum {MAX_BATCH}")
 
 
+def tagged_attn_splits(max_context: int, minimum: int = 1, batch: int = 1) -> int:
+    """Split-KV factor of the tagged persistent kernel: a power of two, at most
+    16 // batch, never below ``minimum``.
+
+    Batch 1 aims at about 120 positions per split (log2 of max_context / 120
+    rounded to the nearest integer), batch 2 at 64 (rounded up), batch 4 and 8
+    at 256 (rounded up, as :func:`auto_attn_splits`). Measured on MI355X (device
+    us per step, tagged kernel, last split folding three partials per poll
+    round): batch 1 at ctx 100: 512 with 1 split, 538 with 2; ctx 480: 545 with
+    4, 579 with 8; ctx 1000: 597 with 8, 629 with 16; ctx 1800: 635 with 16, 661
+    with 8. Batch 2 at ctx 480: 616 with 8, 626 with 4; ctx 1000-1800: 8 best."""
+
+    import math
+
+    b = max(1, int(batch))
+    cap = max(1, MAX_SPLITS // b)
+    ctx = max(1, int(max_context))
+    if b == 1:
+        splits = 1 << max(0, round(math.log2(max(1.0, ctx / 120))))
+    elif b == 2:
+        want = -(-ctx // 64)
+        splits = 1
+        while splits < want:
+            splits *= 2
+    else:
+        return auto_attn_splits(ctx, minimum, b)
+    return max(min(int(minimum), MAX_SPLITS), min(splits, cap))
+
+
 def auto_attn_splits(max_context: int, minimum: int = 1, batch: int = 1) -> int:
     """Split-KV factor: one split per 256 cached positions, a power of two, at most
     16 // batch (so batch x splits <= 16) and never below ``minimum``.

@@ -34,7 +34,7 @@ from nanovllm.model_spec import QWEN3_06B
 from . import native
 from .row_contract import row_active_mask
 from .schedule import (
-    NUM_LAYERS, Schedule, auto_attn_splits, batch_bucket, build_schedule, build_segments, build_stage_schedules,
+    NUM_LAYERS, Schedule, auto_attn_splits, batch_bucket, tagged_attn_splits, build_schedule, build_segments, build_stage_schedules,
 )
 from .verifier import verify
 from .weights import pack_layer_pointers
@@ -456,7 +456,7 @@ class TaskGraphDecoder:
             # both launch modes run the tagged kernel: at most 16 // batch splits (a
             # per-stage launch holds every attention task of the stage co-resident)
             cap = native.MAX_SPLITS // batch_bucket(batch)
-            return min(auto_attn_splits(max_context, self.min_attn_splits, batch_bucket(batch)), cap)
+            return min(tagged_attn_splits(max_context, self.min_attn_splits, batch_bucket(batch)), cap)
         return auto_attn_splits(max_context, self.min_attn_splits, 1)
 
     # -- decode ----------------------------------------------------------------

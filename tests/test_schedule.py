@@ -207,3 +207,14 @@ def test_stage_schedules_one_task_per_workgroup_with_published_residuals():
 
     with pytest.raises(ValueError, match="co-resident"):
         build_stage_schedules(8, 4, num_layers=1, max_grid=256)   # 8 x 16 x 4 = 512 attention tasks
+
+
+def test_tagged_split_rule():
+    """The tagged kernel's measured split rule: ~120 positions per split at batch
+    1 (nearest power of two), 64 at batch 2, 256 at batch 4-8, capped at 16 // batch."""
+    from nanovllm.backends.megakernel.schedule import tagged_attn_splits as t
+
+    assert [t(c) for c in (1, 129, 161, 240, 480, 1000, 1864, 2048)] == [1, 1, 1, 2, 4, 8, 16, 16]
+    assert [t(c, batch=2) for c in (64, 65, 480, 1000, 2048)] == [1, 2, 8, 8, 8]
+    assert [t(c, batch=8) for c in (200, 300, 2048)] == [1, 2, 2] and t(2048, batch=4) == 4
+    assert t(100, minimum=4) == 4 and t(2048, minimum=16, batch=8) == 16
