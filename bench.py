@@ -46,7 +46,7 @@ def step_bytes(contexts: list[int]) -> int:
 
 
 def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="tagged", fusion_groups=1,
-                  attn_splits=1):
+                  attn_splits=1, **options):
     import torch
     from nanovllm.backends.megakernel.taskgraph import TaskGraphDecoder
     from nanovllm.backends.megakernel.weights import weights_from_synthetic
@@ -57,7 +57,7 @@ def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="ta
     kv = torch.zeros(2, num_layers, num_blocks, 256, 8, 128, dtype=torch.bfloat16, device="cuda")
     dec = TaskGraphDecoder(w, k_cache=kv[0], v_cache=kv[1], block_size=256, num_cache_blocks=num_blocks,
                            max_model_len=2048, launch=launch, persistent_variant=variant,
-                           fusion_groups=fusion_groups, attn_splits=attn_splits)
+                           fusion_groups=fusion_groups, attn_splits=attn_splits, **options)
     return synth, w, kv, dec
 
 
@@ -328,6 +328,7 @@ def long_context_runs(workload: str, steps: int, warmup: int, dec=None) -> dict:
                                    "GBps": round(nbytes / us / 1e3, 1),
                                    "floor_us": round(nbytes / HBM_PEAK_GBPS / 1e3, 2),
                                    "splits": dec.splits_for(max(start) + steps + 1, b, mode),
+                                   "pair_heads": dec.pair_heads_for(max(start) + steps + 1, b),
                                    "ctx": [min(start) + 1, max(start) + steps]}
     if own:
         dec.close()

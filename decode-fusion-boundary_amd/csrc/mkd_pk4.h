@@ -1108,11 +1108,17 @@ __device__ __forceinline__ int p4_attn_chunks(const MkdStepDesc& d, const Inst& 
 constexpr float SCALE2 = ATTN_SCALE * 1.4426950408889634f;
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// ATTN task of the tagged kernel: row b, KV head h, query head 2h + g, split
-// `split` of nsplit of the row's positions. Task word a0 = b * 8 + h, plus
-// ATTN_ONE_HEAD and g * ATTN_QHEAD; the two query heads of a KV head are
-// separate tasks (on two workgroups of the KV head's XCD), which halves each
-// task's chain of dependent instructions.
+// ATTN task of the tagged kernel: row b, KV head h, split `split` of nsplit of
+// the row's positions, and either one query head (task word a0 = b * 8 + h,
+// plus ATTN_ONE_HEAD and g * ATTN_QHEAD for head 2h + g) or both (PAIR: a0 =
+// b * 8 + h). One-head tasks put the two query heads of a KV head on two
+// workgroups of the KV head's XCD, which halves each task's chain of dependent
+// instructions (the faster form while the step is latency-bound: short
+// contexts, small batches); a PAIR task reads each K/V chunk once for both
+// heads, half the cache traffic of the one-head form (the faster form once the
+// cache reads bound the step: long contexts at batch 4 and 8). PAIR: wave 3
+// polls, normalizes and ropes the second head's q; each chunk's scores and
+// P * V are computed for both heads from the same K and V reads.
 // The task's cached K/V arrive as KV chunks in the LDS ring (staged by the DMA
 // waves like weight rows), so the compute waves issue no cache loads of their
 // own: their only global loads before the q/k/v poll are the norm weights and
@@ -1166,16 +1172,18 @@ __device__ __forceinline__ void p4_fold_splits(const Ws ws, size_t pbase, int ns
   }
 }
 constexpr int ATTN_QHEAD = 64, ATTN_ONE_HEAD = 128;
+constexpr int P4_PAIR_MIN_B = 4;  // smallest batch whose kernel runs tasks of both query heads
 #ifndef MKD_B1_FOLD_SPR
 #define MKD_B1_FOLD_SPR 3
 #endif  // task word a0 flags (b * 8 + h < 64)
-template <int B, int NS>
+template <int B, int NS, bool PAIR>
 __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int a0, int split, int nsplit,
                                         uint64_t* tr, uint8_t* ring, int cc, int& nch) {
   const int t = p4_tid(), wave = t >> 6, lane = t & 63;
   const uint32_t tag = p4_tag(c.epoch, layer);
-  const int bh = a0 & (ATTN_QHEAD - 1), g = (a0 & ATTN_QHEAD) ? 1 : 0;
-  const int b = bh / NKV, h = bh % NKV, qh = GROUP * h + g;
+  constexpr int NQH = PAIR ? GROUP : 1;  // query heads of this task
+  const int bh = a0 & (ATTN_QHEAD - 1), g = (!PAIR && (a0 & ATTN_QHEAD)) ? 1 : 0;
+  const int b = bh / NKV, h = bh % NKV, qh = GROUP * h + g;  // (PAIR: qh and qh + 1)
   const int bs = d.block_size;
   const int pos_in = b < d.rows ? as_const(d.cache_seqlens)[b] : 0;
   const AttnGeo ag = attn_geo(d.rows, b, pos_in, d.page_stride, bs, split, nsplit);
@@ -1184,22 +1192,25 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   const int pos = ag.pos, p_begin = ag.p_begin, p_end = ag.p_end, c_end = ag.c_end;
   const bool active = ag.live && as_const(d.row_active)[b] != 0;
   const bool writes_kv = g == 0 && split == 0 && active;  // one task stores the new token's K/V
+  const bool qkv_wave = wave < 3 || PAIR;                  // waves that poll a q, k or v word
+  const bool norm_wave = wave < 2 || (PAIR && wave == 3);  // q (waves 0, 3) and k (wave 1): RMSNorm + RoPE
   cint32_t* table = as_const(d.page_table + (size_t)b * d.page_stride);
   const int nblk = d.num_blocks;
   uint8_t* smem = c.attn_smem;
-  uint16_t* qb = reinterpret_cast<uint16_t*>(smem);       // [128] roped q
+  uint16_t* qb = reinterpret_cast<uint16_t*>(smem);       // [128] roped q (head qh)
   uint16_t* kb = qb + HD;                                 // [128] roped k
   uint16_t* vb = kb + HD;                                 // [128] v
-  float* mrg = reinterpret_cast<float*>(smem + 1024);     // [4 waves][128]
-  float* mrg_ml = mrg + PK_CW * HD;                       // [4] m, [4] l
+  uint16_t* qb2 = vb + HD;                                // [128] roped q of head qh + 1 (PAIR)
+  float* mrg = reinterpret_cast<float*>(smem + 1024);     // [4 waves][NQH heads][128]
+  float* mrg_ml = mrg + PK_CW * NQH * HD;                 // [4][NQH] m, then [4][NQH] l
   const size_t layer_off = (size_t)layer * (size_t)d.kv_layer_stride + (size_t)h * HD;
 
   // static operands of the norm/RoPE step and the new token's cache slot: loaded
   // before the poll (the poll's first check then also covers them)
   uint32_t wnw = 0;
   float c0 = 0.f, c1 = 0.f, s0 = 0.f, s1 = 0.f;
-  if (wave < 2) {
-    wnw = ldg(reinterpret_cast<const uint32_t*>(p4_wptr(d, layer, wave == 0 ? MKD_W_Q_NORM : MKD_W_K_NORM)) + lane);
+  if (norm_wave) {
+    wnw = ldg(reinterpret_cast<const uint32_t*>(p4_wptr(d, layer, wave == 1 ? MKD_W_K_NORM : MKD_W_Q_NORM)) + lane);
     const int j = (2 * lane) & 63;
     const float* cs = d.rope_cos + (size_t)pos * (HD / 2);
     const float* sn = d.rope_sin + (size_t)pos * (HD / 2);
@@ -1207,20 +1218,22 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   }
   const int blk_new = writes_kv ? table[pos / bs] : 0;
   const int slot_in_blk = pos % bs;  // (integer division, off the poll's path)
-  // this step's q (wave 0: head qh), k (wave 1), v (wave 2): one word per lane
+  // this step's q (wave 0: head qh; PAIR, wave 3: head qh + 1), k (wave 1), v
+  // (wave 2): one word per lane
   size_t src = TW_QKV + (size_t)b * (QKV_N / 2) + lane;
   if (wave == 0) src += (size_t)qh * (HD / 2);
   else if (wave == 1) src += QS / 2 + (size_t)h * (HD / 2);
-  else src += (QS + KVS) / 2 + (size_t)h * (HD / 2);
+  else if (wave == 2) src += (QS + KVS) / 2 + (size_t)h * (HD / 2);
+  else src += (size_t)(qh + 1) * (HD / 2);
   uint64_t qv[1] = {0};
   bool ok = true;
-  if (wave < 3) ok = poll_tagged<1>([=](int) { return c.ws.tw(src); }, qv, tag, c.ws);
+  if (qkv_wave) ok = poll_tagged<1>([=](int) { return c.ws.tw(src); }, qv, tag, c.ws);
 #ifdef MKD_TRACE_POLL
-  if (tr != nullptr && lane == 0 && wave < 3) atomicMax(reinterpret_cast<unsigned long long*>(tr + 1), (unsigned long long)wall_clock64());
+  if (tr != nullptr && lane == 0 && qkv_wave) atomicMax(reinterpret_cast<unsigned long long*>(tr + 1), (unsigned long long)wall_clock64());
 #endif
   const uint32_t word = (uint32_t)qv[0];  // dims 2*lane, 2*lane + 1
   uint32_t outw = word;
-  if (wave < 2) {
+  if (norm_wave) {
     const float x0 = bf_lo(word), x1 = bf_hi(word);
     const float ss = wave_sum(x0 * x0 + x1 * x1);
     const float r = __builtin_amdgcn_rsqf(ss * (1.0f / HD) + EPS);
@@ -1239,7 +1252,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     outw = pack_bf2(o0, o1);
   }
   p4_trace_at(c, 4);
-  if (wave < 3) reinterpret_cast<uint32_t*>(wave == 0 ? qb : (wave == 1 ? kb : vb))[lane] = outw;
+  if (qkv_wave) reinterpret_cast<uint32_t*>(qb + wave * HD)[lane] = outw;  // qb, kb, vb, qb2
   // the new token's K (wave 1) and V (wave 2) go to their cache slot from registers
   if (writes_kv && (wave == 1 || wave == 2)) {
     if (blk_new < 0 || blk_new >= nblk) {
@@ -1261,20 +1274,25 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   }
   if (tr != nullptr && t == 0) tr[2] = wall_clock64();
 
-  // scores layout: this lane's 16 dims of q
+  // scores layout: this lane's 16 dims of q (PAIR: of both query heads)
   const int pl = lane >> 3, part = lane & 7;
-  uint4 qa[2];
+  uint4 qa[2], qc[2];
 #pragma unroll
-  for (int i = 0; i < 2; i++) qa[i] = reinterpret_cast<const uint4*>(qb + part * 16)[i];
+  for (int i = 0; i < 2; i++) {
+    qa[i] = reinterpret_cast<const uint4*>(qb + part * 16)[i];
+    qc[i] = PAIR ? reinterpret_cast<const uint4*>(qb2 + part * 16)[i] : make_uint4(0, 0, 0, 0);
+  }
   // Online softmax with a lazily raised reference maximum m0: the
   // probabilities are 2^(score - m0), and m0 (with the sums and the output
   // accumulators) is rescaled only when a score exceeds it by more than
   // LAZY_LOG2 (so every probability stays below 2^LAZY_LOG2). The sum of
   // probabilities is kept per lane (the lanes with part 0, one per position)
-  // and reduced once after the loop.
+  // and reduced once after the loop. PAIR: the second query head keeps its own
+  // m1, sum and accumulators; the two heads share each K/V read from LDS.
   constexpr float LAZY_LOG2 = 8.f;
-  float m0 = -INFINITY, ls = 0.f;
+  float m0 = -INFINITY, ls = 0.f, m1 = -INFINITY, ls1 = 0.f;
   float a00 = 0.f, a01 = 0.f;  // dims 2 lane, 2 lane + 1
+  float a10 = 0.f, a11 = 0.f;  // (PAIR: head qh + 1)
   const uint8_t* slot = ring + (cc % NS) * SLOT_BYTES;
   const uint8_t* const ring_end = ring + NS * SLOT_BYTES;
   const int pp = 8 * wave + pl;  // this lane's position within a chunk
@@ -1283,8 +1301,10 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     const uint4 k0 = *reinterpret_cast<const uint4*>(slot + kv_kpiece(pp, 2 * part));
     const uint4 k1 = *reinterpret_cast<const uint4*>(slot + kv_kpiece(pp, 2 * part + 1));
     float sc0 = sum_within_8(dot8(k1, qa[1], dot8(k0, qa[0], 0.f)));
+    float sc1 = PAIR ? sum_within_8(dot8(k1, qc[1], dot8(k0, qc[0], 0.f))) : 0.f;
     const bool valid = p_begin + KV_CHUNK * j + pp < c_end;
     sc0 = valid ? sc0 * SCALE2 : -INFINITY;
+    sc1 = valid ? sc1 * SCALE2 : -INFINITY;
     // (m0 = -inf: any valid score raises it; invalid scores never do)
     if (__builtin_amdgcn_ballot_w64(sc0 > m0 + LAZY_LOG2) != 0) {
       const float n0 = fmaxf(m0, max_over_8_groups(sc0));
@@ -1292,34 +1312,57 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
       ls *= al0; a00 *= al0; a01 *= al0;
       m0 = n0;
     }
+    if (PAIR && __builtin_amdgcn_ballot_w64(sc1 > m1 + LAZY_LOG2) != 0) {
+      const float n1 = fmaxf(m1, max_over_8_groups(sc1));
+      const float al1 = m1 == -INFINITY ? 0.f : ex2(m1 - n1);
+      ls1 *= al1; a10 *= al1; a11 *= al1;
+      m1 = n1;
+    }
     // (a wave whose positions are all past c_end keeps m = -inf, sums 0)
     const float e0 = valid ? ex2(sc0 - m0) : 0.f;
+    const float e1 = PAIR && valid ? ex2(sc1 - m1) : 0.f;
     ls += part == 0 ? e0 : 0.f;
+    ls1 += part == 0 ? e1 : 0.f;
 #pragma unroll
     for (int q = 0; q < 8; q++) {
       const float w0 = lane_value(e0, 8 * q);
       const uint32_t vw = *reinterpret_cast<const uint32_t*>(slot + KV_V_OFF + (8 * wave + q) * 256 + 4 * lane);
       a00 += w0 * bf_lo(vw); a01 += w0 * bf_hi(vw);
+      if constexpr (PAIR) {
+        const float w1 = lane_value(e1, 8 * q);
+        a10 += w1 * bf_lo(vw); a11 += w1 * bf_hi(vw);
+      }
     }
     slot += SLOT_BYTES;
     if (slot == ring_end) slot = ring;
   }
   float l0 = wave_sum(ls);
+  float l1 = PAIR ? wave_sum(ls1) : 0.f;
   // the token's own position (wave 3: it has the fewest cached positions in the last chunk)
   if (wave == PK_CW - 1 && p_begin <= pos && pos < p_end) {
     const uint32_t kw = reinterpret_cast<const uint32_t*>(kb)[lane];
-    const float t0s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb)[lane], 0.f)) * SCALE2;
-    const float n0 = fmaxf(m0, t0s);
-    const float al0 = ex2(m0 - n0), e0 = ex2(t0s - n0);
-    l0 = l0 * al0 + e0;
-    m0 = n0;
     const uint32_t vw = reinterpret_cast<const uint32_t*>(vb)[lane];
-    a00 = a00 * al0 + e0 * bf_lo(vw); a01 = a01 * al0 + e0 * bf_hi(vw);
+    {
+      const float t0s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb)[lane], 0.f)) * SCALE2;
+      const float n0 = fmaxf(m0, t0s);
+      const float al0 = ex2(m0 - n0), e0 = ex2(t0s - n0);
+      l0 = l0 * al0 + e0;
+      m0 = n0;
+      a00 = a00 * al0 + e0 * bf_lo(vw); a01 = a01 * al0 + e0 * bf_hi(vw);
+    }
+    if constexpr (PAIR) {
+      const float t1s = wave_sum(dot2(kw, reinterpret_cast<const uint32_t*>(qb2)[lane], 0.f)) * SCALE2;
+      const float n1 = fmaxf(m1, t1s);
+      const float al1 = ex2(m1 - n1), e1 = ex2(t1s - n1);
+      l1 = l1 * al1 + e1;
+      m1 = n1;
+      a10 = a10 * al1 + e1 * bf_lo(vw); a11 = a11 * al1 + e1 * bf_hi(vw);
+    }
   }
   const size_t pbase = TW_APART + (((size_t)b * NKV + h) * MAXS) * PART_STRIDE;  // split partials of (b, h)
   // (batch 2 and 4: inlined at batch 1 and 8, where it never helps a short
   // context, this code slowed the short-context step: 8-15 us, measured)
-  constexpr bool FOLD = B == 2 || B == 4;
+  constexpr bool FOLD = !PAIR && (B == 2 || B == 4);
   if constexpr (FOLD) {
     if (nsplit > 1 && split == nsplit - 1) {
       // last split: wave w folds the other splits' partials into its own
@@ -1328,40 +1371,47 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     }
   }
   // merge the waves in LDS
-  reinterpret_cast<float2*>(mrg + wave * HD)[lane] = make_float2(a00, a01);
-  if (lane == 0) { mrg_ml[wave] = m0; mrg_ml[PK_CW + wave] = l0; }
+  reinterpret_cast<float2*>(mrg + wave * NQH * HD)[lane] = make_float2(a00, a01);
+  if (PAIR) reinterpret_cast<float2*>(mrg + wave * NQH * HD + HD)[lane] = make_float2(a10, a11);
+  if (lane == 0) {
+    mrg_ml[wave * NQH] = m0; mrg_ml[PK_CW * NQH + wave * NQH] = l0;
+    if (PAIR) { mrg_ml[wave * NQH + 1] = m1; mrg_ml[PK_CW * NQH + wave * NQH + 1] = l1; }
+  }
   c.sync();
   // thread t: dim dd of the head; threads t and t + 128 compute the same value
+  // (PAIR: thread t of head qh + (t >> 7), gg = its query head within the group)
   const int dd = t & (HD - 1), half = t >> 7;
+  const int hh = PAIR ? half : 0, gg = PAIR ? half : g;
   float M = -INFINITY;
 #pragma unroll
-  for (int ww = 0; ww < PK_CW; ww++) M = fmaxf(M, mrg_ml[ww]);
+  for (int ww = 0; ww < PK_CW; ww++) M = fmaxf(M, mrg_ml[ww * NQH + hh]);
   float num = 0.f, den = 0.f;
   if (M != -INFINITY) {
 #pragma unroll
     for (int ww = 0; ww < PK_CW; ww++) {
-      const float sc = ex2(mrg_ml[ww] - M);
-      num += mrg[ww * HD + dd] * sc;
-      den += mrg_ml[PK_CW + ww] * sc;
+      const float sc = ex2(mrg_ml[ww * NQH + hh] - M);
+      num += mrg[(ww * NQH + hh) * HD + dd] * sc;
+      den += mrg_ml[PK_CW * NQH + ww * NQH + hh] * sc;
     }
   }
   if (nsplit > 1 && split != nsplit - 1) {
     // read only by the last split of this (row, query head)
     uint64_t* part = c.ws.tw(pbase + (size_t)split * PART_STRIDE);
-    if (half == 0) {
-      st_tw(part + g * HD + dd, tw_make(__float_as_uint(num), tag));
+    if (PAIR || half == 0) {
+      st_tw(part + gg * HD + dd, tw_make(__float_as_uint(num), tag));
       if (dd == 0) {
-        st_tw(part + GROUP * HD + g, tw_make(__float_as_uint(M), tag));
-        st_tw(part + GROUP * HD + GROUP + g, tw_make(__float_as_uint(den), tag));
+        st_tw(part + GROUP * HD + gg, tw_make(__float_as_uint(M), tag));
+        st_tw(part + GROUP * HD + GROUP + gg, tw_make(__float_as_uint(den), tag));
       }
     }
     c.sync();  // the scratch is reused by this workgroup's next task
     return true;
   }
-  if constexpr (B == 1) {
-    // batch 1: the last split folds the other splits' partials here, up to
-    // SPR splits per poll round (all of a round's loads in flight at once:
-    // one round trip instead of one per split), in split order
+  if constexpr (B == 1 || PAIR) {
+    // batch 1 (and tasks of both query heads): the last split folds the other
+    // splits' partials here, up to SPR splits per poll round (all of a round's
+    // loads in flight at once: one round trip instead of one per split), in
+    // split order
     constexpr int SPR = MKD_B1_FOLD_SPR;
     for (int sp0 = 0; nsplit > 1 && sp0 < nsplit - 1; sp0 += SPR) {
       uint64_t e[3 * SPR];
@@ -1370,7 +1420,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
                      [&](int k) {
                        const int sp = min(sp0 + k / 3, nsplit - 2), f = k % 3;
                        const size_t ps = pbase + (size_t)sp * PART_STRIDE;
-                       return c.ws.tw(ps + (f == 0 ? (size_t)(g * HD + dd) : (size_t)(GROUP * HD + (f - 1) * GROUP + g)));
+                       return c.ws.tw(ps + (f == 0 ? (size_t)(gg * HD + dd) : (size_t)(GROUP * HD + (f - 1) * GROUP + gg)));
                      },
                      e, tag, c.ws);
 #pragma unroll
@@ -1387,7 +1437,7 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
       }
     }
   }
-  if constexpr (B == 8) {
+  if constexpr (B == 8 && !PAIR) {
     // batch 8: the last split folds the other splits' partials here, one
     // split per round; the two thread halves (the same dims) take the even and
     // the odd splits, then combine (even, odd) in that order
@@ -1442,10 +1492,12 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     // the pair (dd, dd + 1) as one word; its 8 replicas are stored by the four
     // threads (dd even / odd, half 0 / 1) that hold it, two each
     const uint64_t v = tw_make((dd & 1) ? (nbr | (mine << 16)) : (mine | (nbr << 16)), tag);
-    const size_t word = TW_ATTN + (size_t)b * (QS / 2) + ((size_t)qh * HD + dd) / 2;
-    const int r0 = ((dd & 1) * 2 + half) * (TW_NREP / 4);
+    // (PAIR: two threads, dd even / odd, four each)
+    constexpr int NR = PAIR ? TW_NREP / 2 : TW_NREP / 4;
+    const size_t word = TW_ATTN + (size_t)b * (QS / 2) + ((size_t)(qh + hh) * HD + dd) / 2;
+    const int r0 = PAIR ? (dd & 1) * NR : ((dd & 1) * 2 + half) * NR;
 #pragma unroll
-    for (int r = 0; r < TW_NREP / 4; r++) st_rep(c.ws, word, r0 + r, v);
+    for (int r = 0; r < NR; r++) st_rep(c.ws, word, r0 + r, v);
   }
   return p4_agree(c, ok);  // also frees the scratch for the next task
 }
@@ -1786,12 +1838,21 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
     if (w.op == MKD_OP_QKV || w.op == MKD_OP_GATEUP) c.par ^= 1;
     if (w.op == MKD_OP_ATTN) {
       int nkv = 0;
-      if (!aborted && !(w.a0 & ATTN_ONE_HEAD)) {  // a task of both query heads: not this kernel's schedule
+      // ATTN_ONE_HEAD: one query head per task, else both heads of the KV head
+      // (compiled from batch P4_PAIR_MIN_B on: at batch 1 the second body alone,
+      // never run, slowed the step by 2%, measured)
+      const bool pair = !(w.a0 & ATTN_ONE_HEAD);
+      if (!aborted && pair && B < P4_PAIR_MIN_B) {
         if (threadIdx.x == 0) st_co(ws.line(CTR_ERR), ERR_BAD_INST);
         aborted = true;
       }
       if (!aborted) {
-        aborted = !p4_attn<B, Cfg::NS>(d, c, w.layer, w.a0, w.a1, w.a2, tr, ring, cc, nkv);
+        if constexpr (B >= P4_PAIR_MIN_B) {
+          aborted = pair ? !p4_attn<B, Cfg::NS, true>(d, c, w.layer, w.a0, w.a1, w.a2, tr, ring, cc, nkv)
+                         : !p4_attn<B, Cfg::NS, false>(d, c, w.layer, w.a0, w.a1, w.a2, tr, ring, cc, nkv);
+        } else {
+          aborted = !p4_attn<B, Cfg::NS, false>(d, c, w.layer, w.a0, w.a1, w.a2, tr, ring, cc, nkv);
+        }
       } else {
         nkv = p4_attn_chunks(d, w);
         p4_skip_chunks<Cfg::NS>(cc, nkv);

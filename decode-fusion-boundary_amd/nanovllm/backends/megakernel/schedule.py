@@ -75,7 +75,26 @@ def batch_bucket(rows: int) -> int:
     raise ValueError(f"batch {rows} exceeds the compiled maximum {MAX_BATCH}")
 
 
-def tagged_attn_splits(max_context: int, minimum: int = 1, batch: int = 1) -> int:
+PAIR_HEADS_MIN_BATCH = 4         # smallest batch bucket whose tagged kernel runs tasks of both query heads
+PAIR_HEADS_MIN_CONTEXT = 257     # and the shortest step context at which they are used
+PAIR_POSITIONS_PER_SPLIT = 256   # cached positions per split they aim at
+
+
+def tagged_pair_heads(batch: int, max_context: int) -> bool:
+    """Whether the tagged kernel's attention tasks cover both query heads of
+    their KV head (each cached K/V chunk read once) rather than one (the chunk
+    read by two tasks, each with half the dependent work).
+
+    Measured on MI355X (device us per step, tagged kernel): batch 8, C5 contexts
+    (~1100-1900): 1426 one-head (2 splits) -> 1224 both heads (4 splits); C4
+    (ctx ~520): 1073 -> 1046; batch 4, C5: 932 -> 912; but at short contexts
+    (ctx < 100) one-head tasks are faster (batch 8: 894 vs 911, batch 4: 694 vs
+    706), and at batch 2, C5: 710 one-head vs 765 both heads."""
+
+    return int(batch) >= PAIR_HEADS_MIN_BATCH and int(max_context) >= PAIR_HEADS_MIN_CONTEXT
+
+
+def tagged_attn_splits(max_context: int, minimum: int = 1, batch: int = 1, pair_heads: bool = False) -> int:
     """Split-KV factor of the tagged persistent kernel: a power of two, at most
     16 // batch, never below ``minimum``.
 
@@ -92,6 +111,14 @@ def tagged_attn_splits(max_context: int, minimum: int = 1, batch: int = 1) -> in
     b = max(1, int(batch))
     cap = max(1, MAX_SPLITS // b)
     ctx = max(1, int(max_context))
+    if pair_heads:
+        # half the tasks per split: up to 32 // batch splits (at most 16)
+        cap = max(1, min(MAX_SPLITS, 2 * MAX_SPLITS // b))
+        want = max(1, -(-ctx // PAIR_POSITIONS_PER_SPLIT))
+        splits = 1
+        while splits < want and splits < cap:
+            splits *= 2
+        return max(min(int(minimum), MAX_SPLITS), splits)
     if b == 1:
         splits = 1 << max(0, round(math.log2(max(1.0, ctx / 120))))
     elif b == 2:
@@ -228,10 +255,12 @@ def _qkv_segments():
 
 
 def build_stages(batch: int, attn_splits: int, num_wgs: int,
-                 num_layers: int = NUM_LAYERS, q_head_tasks: bool = False) -> list[Stage]:
+                 num_layers: int = NUM_LAYERS, q_head_tasks: bool = False,
+                 pair_heads: bool = False) -> list[Stage]:
     """The step's stages in dependency order. ``q_head_tasks`` (the tagged
     kernel's schedule) makes one ATTN task per query head instead of per KV
-    head: task word a0 = b * 8 + h + ATTN_ONE_HEAD (+ ATTN_QHEAD for head 2h + 1)."""
+    head: task word a0 = b * 8 + h + ATTN_ONE_HEAD (+ ATTN_QHEAD for head 2h + 1),
+    unless ``pair_heads`` keeps one task per KV head (a0 = b * 8 + h)."""
 
     if batch not in BATCH_BUCKETS:
         raise ValueError(f"batch bucket must be one of {BATCH_BUCKETS}; got {batch}")
@@ -255,7 +284,7 @@ def build_stages(batch: int, attn_splits: int, num_wgs: int,
                 per_head[h] += 1
         stages.append(qkv)
         attn = Stage(OP_ATTN, layer)
-        heads = ([ATTN_ONE_HEAD, ATTN_ONE_HEAD | ATTN_QHEAD] if q_head_tasks else [0])
+        heads = ([ATTN_ONE_HEAD, ATTN_ONE_HEAD | ATTN_QHEAD] if q_head_tasks and not pair_heads else [0])
         for b in range(batch):
             for h in range(NUM_KV_HEADS):
                 for s in range(attn_splits):
@@ -356,13 +385,13 @@ def split_layers(num_layers: int, groups: int) -> list[tuple[int, int]]:
 
 
 def build_segments(batch: int, attn_splits: int, num_wgs: int, num_layers: int = NUM_LAYERS,
-                   groups: int = 1, q_head_tasks: bool = False) -> list[Schedule]:
+                   groups: int = 1, q_head_tasks: bool = False, pair_heads: bool = False) -> list[Schedule]:
     """One persistent launch per layer segment. Segment ``k`` holds the stages of
     its layers (the last one also the LM head); its first QKV stage waits on the
     previous segment's down counter, which the earlier launch already completed,
     and the final LM-head task clears every fan-in counter of the step."""
 
-    stages = build_stages(batch, attn_splits, num_wgs, num_layers, q_head_tasks)
+    stages = build_stages(batch, attn_splits, num_wgs, num_layers, q_head_tasks, pair_heads)
     out = []
     for start, end in split_layers(num_layers, groups):
         seg = [s for s in stages if start <= s.layer < end or (end == num_layers and s.op == OP_LMHEAD)]
@@ -377,7 +406,7 @@ def build_segments(batch: int, attn_splits: int, num_wgs: int, num_layers: int =
 
 
 def build_stage_schedules(batch: int, attn_splits: int, num_layers: int = NUM_LAYERS,
-                          max_grid: int = 256) -> list[Schedule]:
+                          max_grid: int = 256, pair_heads: bool = False) -> list[Schedule]:
     """The per-op comparator on the tagged persistent kernel's own task bodies:
     one persistent launch per stage, one task per workgroup (``grid`` = the
     stage's task count). Every QKV task publishes the residual after the input
@@ -388,7 +417,7 @@ def build_stage_schedules(batch: int, attn_splits: int, num_layers: int = NUM_LA
     tasks."""
 
     out = []
-    for st in build_stages(batch, attn_splits, max_grid, num_layers, q_head_tasks=True):
+    for st in build_stages(batch, attn_splits, max_grid, num_layers, q_head_tasks=True, pair_heads=pair_heads):
         flag = QKV_PUBLISH_RES if st.op == OP_QKV else (GATEUP_PUBLISH_RES if st.op == OP_GATEUP else 0)
         tasks = [dataclasses.replace(t, a2=t.a2 | flag) for t in st.tasks] if flag else list(st.tasks)
         if len(tasks) > max_grid:

@@ -34,7 +34,8 @@ from nanovllm.model_spec import QWEN3_06B
 from . import native
 from .row_contract import row_active_mask
 from .schedule import (
-    NUM_LAYERS, Schedule, auto_attn_splits, batch_bucket, tagged_attn_splits, build_schedule, build_segments, build_stage_schedules,
+    NUM_LAYERS, PAIR_HEADS_MIN_BATCH, Schedule, auto_attn_splits, batch_bucket, build_schedule, build_segments,
+    build_stage_schedules, tagged_attn_splits, tagged_pair_heads,
 )
 from .verifier import verify
 from .weights import pack_layer_pointers
@@ -143,7 +144,7 @@ class _Geometry:
 def _check_tagged_preconditions(segs) -> None:
     """What the tagged-exchange kernel relies on: GEMV row blocks of even size at
     even offsets (a word carries two values of one task), at most 32 rows per
-    block (its result tile), one query head per attention task, and an LM-head
+    block (its result tile), and an LM-head
     task on every workgroup of the last launch (the last LM slot advances the step counter once every workgroup has
     read it). Every workgroup also runs exactly one QKV and one gate/up task per
     layer of a launch: each keeps the residual stream in registers, updates it in
@@ -172,8 +173,6 @@ def _check_tagged_preconditions(segs) -> None:
                     rows = 2 * t.a1 if t.op in (native.OP_GATEUP, native.OP_DOWN) else t.a1
                     if t.a0 % 2 or t.a1 % 2 or rows > 32:
                         raise RuntimeError(f"task {t} does not fit the tagged exchange (even blocks of <= 32 rows)")
-                if t.op == native.OP_ATTN and not t.a0 & native.ATTN_ONE_HEAD:
-                    raise RuntimeError(f"task {t}: the tagged kernel runs one query head per attention task")
     last = segs[-1]
     if any(not any(t.op == native.OP_LMHEAD for t in row) for row in last.rows):
         raise RuntimeError("the tagged exchange needs an LM-head task on every workgroup")
@@ -185,7 +184,8 @@ class TaskGraphDecoder:
     def __init__(self, weights: dict, *, k_cache, v_cache, block_size: int, num_cache_blocks: int,
                  max_model_len: int, attn_splits: int = 1, fusion_groups: int = 1,
                  launch: str = "persistent", verbose: bool = False, debug_bounds: bool = False,
-                 persistent_variant: str = "tagged", binding: str = "ctypes"):
+                 persistent_variant: str = "tagged", binding: str = "ctypes",
+                 attn_pair_heads: bool | None = None):
         self._lib = native.load()
         if binding not in ("ctypes", "torch_ops"):
             raise ValueError(f"binding must be 'ctypes' or 'torch_ops'; got {binding!r}")
@@ -228,6 +228,9 @@ class TaskGraphDecoder:
         if not 1 <= attn_splits <= MAX_ATTN_SPLITS:
             raise ValueError(f"attn_splits must be 1..{MAX_ATTN_SPLITS}; got {attn_splits}")
         self.min_attn_splits = int(attn_splits)
+        # tagged kernel: attention tasks of both query heads of a KV head (one read
+        # of each K/V chunk) or of one query head; None: tagged_pair_heads(batch)
+        self.attn_pair_heads = attn_pair_heads
         self.fusion_groups = int(fusion_groups)
         if not 1 <= self.fusion_groups <= self.num_layers:
             raise ValueError(f"fusion_groups must be in [1, {self.num_layers}]; got {fusion_groups}")
@@ -279,11 +282,11 @@ class TaskGraphDecoder:
         )
         self._stream_ptr()
         native.check(self._lib.mkd_reset_counters(native.ctypes.byref(self._desc), self._stream_ptr()))
-        self._geometries: dict[tuple[int, int], _Geometry] = {}
+        self._geometries: dict[tuple[int, int, bool], _Geometry] = {}
         for b in (1, 2, 4, 8):
             self._geometry(b, self.min_attn_splits)
         if verbose:
-            g = self._geometries[(1, self.min_attn_splits)]
+            g = self._geometries[(1, self.min_attn_splits, False)]
             print(f"taskgraph decoder: grid={self.grid} launch={self.launch} layers={self.num_layers} "
                   f"fusion_groups={self.fusion_groups} max_pages={self.max_pages} "
                   f"tasks(B=1)={sum(s.num_tasks for s in g.segments)}")
@@ -292,13 +295,17 @@ class TaskGraphDecoder:
     def _stream_ptr(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
-    def _geometry(self, batch: int, splits: int) -> _Geometry:
-        key = (batch, splits)
+    def _geometry(self, batch: int, splits: int, pair: bool = False) -> _Geometry:
+        """Schedules of one (batch bucket, split-KV factor, attention task form)."""
+
+        key = (batch, splits, bool(pair))
         geo = self._geometries.get(key)
         if geo is not None:
             return geo
         tagged = bool(self._variant_flags & native.FLAG_PK_TAGGED)
-        segs = build_segments(batch, splits, self.grid, self.num_layers, self.fusion_groups, q_head_tasks=tagged)
+        pair = tagged and bool(pair)
+        segs = build_segments(batch, splits, self.grid, self.num_layers, self.fusion_groups, q_head_tasks=tagged,
+                              pair_heads=pair)
         whole = build_schedule(batch, splits, self.grid, self.num_layers)
         errors = verify(whole)
         if errors:
@@ -319,7 +326,8 @@ class TaskGraphDecoder:
         geo = _Geometry(batch=batch, attn_splits=splits, segments=segs, persistent=persistent,
                         stage_inst=stage_inst, stages=stages, num_stages=len(table))
         try:
-            stage_scheds = build_stage_schedules(batch, splits, self.num_layers, max_grid=self.grid) if tagged else []
+            stage_scheds = (build_stage_schedules(batch, splits, self.num_layers, max_grid=self.grid, pair_heads=pair)
+                            if tagged else [])
         except ValueError:
             stage_scheds = []   # a stage too large to be co-resident: the generic per-op kernels serve it
         if stage_scheds:
@@ -445,19 +453,39 @@ class TaskGraphDecoder:
             raise native.MegakernelError(f"decode step failed on the device (error {err}: {kind})")
         return status[16:16 + rows].tolist()
 
+    def pair_heads_for(self, max_context: int, batch: int = 1) -> bool:
+        """Whether the tagged kernel's attention tasks of a step cover both query
+        heads of a KV head: :func:`tagged_pair_heads` of the batch bucket and the
+        step's longest context, or, when forced (``attn_pair_heads``), at every
+        bucket whose kernel runs them."""
+
+        if self.persistent_variant != "tagged":
+            return False
+        bucket = batch_bucket(batch)
+        if self.attn_pair_heads is not None:
+            return bool(self.attn_pair_heads) and bucket >= PAIR_HEADS_MIN_BATCH
+        return tagged_pair_heads(bucket, max_context)
+
     def splits_for(self, max_context: int, batch: int = 1, mode: str | None = None) -> int:
         """Split-KV factor for a step. The tagged kernel (persistent, and its per-op
-        launches) caps splits at 16 // batch bucket; the generic per-op stage kernels
-        (lds_dma variant) need many workgroups per launch and keep one split per 256
-        positions (measured at C5, batch 8: 2358 us per step with 8 splits, 2692 us
-        with 2)."""
+        launches) keeps a stage's attention tasks within one task per workgroup
+        (16 // batch bucket splits, 32 // batch with tasks of both query heads, at
+        most 16); the generic per-op stage kernels (lds_dma variant) need many
+        workgroups per launch and keep one split per 256 positions (measured at C5,
+        batch 8: 2358 us per step with 8 splits, 2692 us with 2)."""
 
         if self.persistent_variant == "tagged":
-            # both launch modes run the tagged kernel: at most 16 // batch splits (a
-            # per-stage launch holds every attention task of the stage co-resident)
-            cap = native.MAX_SPLITS // batch_bucket(batch)
-            return min(tagged_attn_splits(max_context, self.min_attn_splits, batch_bucket(batch)), cap)
+            bucket = batch_bucket(batch)
+            pair = self.pair_heads_for(max_context, bucket)
+            return tagged_attn_splits(max_context, self.min_attn_splits, bucket, pair_heads=pair)
         return auto_attn_splits(max_context, self.min_attn_splits, 1)
+
+    def geometry_for(self, max_context: int, rows: int, mode: str | None = None) -> _Geometry:
+        """The schedules a step of ``rows`` rows whose longest context is
+        ``max_context`` runs: batch bucket, split-KV factor, attention task form."""
+
+        return self._geometry(batch_bucket(rows), self.splits_for(max_context, rows, mode),
+                              self.pair_heads_for(max_context, rows))
 
     # -- decode ----------------------------------------------------------------
     def decode_rows(self, input_ids, positions, block_tables, active_rows=None, logits=None,
@@ -480,7 +508,7 @@ class TaskGraphDecoder:
             raise ValueError(
                 f"block table has {cols} columns but the task-graph page_table stride is "
                 f"{self.max_pages} (max_model_len // block_size)")
-        geo = self._geometry(batch_bucket(rows), self.splits_for(cols * self.block_size, rows, mode))
+        geo = self.geometry_for(cols * self.block_size, rows, mode)
         if self.debug_bounds:
             self._audit_device_rows(input_ids, positions, block_tables, geo)
         self._ids[:rows].copy_(input_ids)
@@ -514,7 +542,7 @@ class TaskGraphDecoder:
         if self._mask_dirty:
             self._row_active.fill_(1)
             self._mask_dirty = False
-        geo = self._geometry(1, self.splits_for(cols * self.block_size))
+        geo = self.geometry_for(cols * self.block_size, 1)
         self._launch(self._desc_for(1, geo), geo)
         return int(self._read_status(1)[0])
 
@@ -550,7 +578,7 @@ class TaskGraphDecoder:
         if self._mask_dirty:
             self._row_active.fill_(1)
             self._mask_dirty = False
-        geo = self._geometry(batch_bucket(rows), self.splits_for(cols * self.block_size, rows))
+        geo = self.geometry_for(cols * self.block_size, rows)
         self._launch(self._desc_for(rows, geo), geo)
         return self._read_status(rows)
 
@@ -578,7 +606,7 @@ class TaskGraphDecoder:
         """Return a zero-argument callable that runs one device-resident step
         (token fed back, position advanced on the device, no host sync)."""
 
-        geo = self._geometry(batch_bucket(rows), self.splits_for(max_context, rows, mode))
+        geo = self.geometry_for(max_context, rows, mode)
         desc = self._desc_for(rows, geo, flags=native.FLAG_ADVANCE)
         if mode == "graph":
             handle = self._capture(desc, geo, self._stream_ptr())

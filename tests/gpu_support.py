@@ -16,7 +16,7 @@ class Harness:
 
     def __init__(self, num_layers: int, num_blocks: int, *, launch="persistent", attn_splits=1,
                  fusion_groups=1, max_model_len=2048, kv_fill_seed: int | None = None,
-                 variant: str = "lds_dma"):
+                 variant: str = "lds_dma", **decoder_options):
         from nanovllm.backends.megakernel.taskgraph import TaskGraphDecoder
         from nanovllm.backends.megakernel.weights import weights_from_synthetic
         from oracle.qwen3_oracle import Oracle
@@ -35,7 +35,7 @@ class Harness:
         self.dec = TaskGraphDecoder(self.w, k_cache=self.kv[0], v_cache=self.kv[1], block_size=BS,
                                     num_cache_blocks=num_blocks, max_model_len=max_model_len,
                                     attn_splits=attn_splits, fusion_groups=fusion_groups, launch=launch,
-                                    persistent_variant=variant)
+                                    persistent_variant=variant, **decoder_options)
         self.oracle = Oracle(self.synth)
 
     def step(self, ids, positions, tables, active=None, mode=None):

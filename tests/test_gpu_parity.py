@@ -272,6 +272,73 @@ def test_batch8_long_ragged_context(mode, variant):
     h.close()
 
 
+def _ragged(batch, num_blocks, seed):
+    """Ragged contexts up to ~1.9k positions on scattered pages of 256."""
+    pos = [1900, 1500, 1023, 700, 300, 1777, 64, 1200][:batch]
+    ids = [3, 151935, 42, 9000, 123, 77777, 5, 60000][:batch]
+    perm = torch.randperm(num_blocks, generator=torch.Generator().manual_seed(seed)).tolist()
+    tables = []
+    for p in pos:
+        n = p // 256 + 1
+        tables.append(perm[:n])
+        perm = perm[n:]
+    return ids, pos, tables
+
+
+@pytest.mark.parametrize("batch", [4, 8])
+def test_pair_head_attention_matches_one_head_bitwise(batch):
+    """Tagged kernel, one split: attention tasks of both query heads of a KV head
+    compute each head exactly as the one-head tasks do (same position order,
+    same lazy maxima, same wave merge), so logits and the KV cache are bitwise
+    equal. (With several splits the two forms fold the split partials in a
+    different order; the long ragged test below bounds both against the oracle.)"""
+    print(f"case: pair-head vs one-head attention, batch {batch}, one split", flush=True)
+    ids, pos, tables = _ragged(batch, 48, seed=23)
+    out = []
+    for pair in (False, True):
+        h = Harness(num_layers=2, num_blocks=48, kv_fill_seed=11, variant="tagged", attn_pair_heads=pair)
+        h.dec.splits_for = lambda *args, **kw: 1
+        assert h.dec.pair_heads_for(max(pos) + 1, batch) == pair
+        toks, logits = h.step(ids, pos, tables)
+        out.append((toks, logits, h.kv.cpu()))
+        h.close()
+    assert out[0][0] == out[1][0]
+    assert torch.equal(out[0][1], out[1][1]), f"logits differ: {max_abs(out[0][1], out[1][1])}"
+    assert torch.equal(out[0][2], out[1][2])
+
+
+def test_pair_head_tasks_rejected_below_batch_4():
+    """The batch-1 and batch-2 kernels are built without the two-head attention
+    body: forcing it there leaves the decoder on one-head tasks."""
+    h = Harness(num_layers=1, num_blocks=8, variant="tagged", attn_pair_heads=True)
+    assert not h.dec.pair_heads_for(2000, 2) and h.dec.pair_heads_for(2000, 4)
+    h.close()
+
+
+@pytest.mark.parametrize("batch", [2, 4, 8])
+@pytest.mark.parametrize("pair", [False, True])
+def test_pair_and_one_head_attention_long_ragged(batch, pair):
+    """Tagged kernel, ragged contexts up to 1.9k at batch 2/4/8, with attention
+    tasks of one or of both query heads (each at its own split rule), against
+    the oracle with the torch-relative bound; KV slots exact."""
+    print(f"case: long ragged context, batch {batch}, pair heads {pair}", flush=True)
+    h = Harness(num_layers=2, num_blocks=48, kv_fill_seed=13, variant="tagged", attn_pair_heads=pair)
+    h.kv_before = h.kv_cpu.clone()
+    ids, pos, tables = _ragged(batch, 48, seed=17)
+    toks, logits = h.step(ids, pos, tables)
+    ref_toks, ref_logits = h.oracle_step(ids, pos, tables)
+    torch_logits = _torch_path_logits(2, h.kv_before, ids, pos, tables)
+    err = max_abs(logits, ref_logits)
+    err_torch = max_abs(torch_logits, ref_logits)
+    bound = LOGIT_TOL + 1.5 * err_torch
+    print(f"  splits={h.dec.splits_for(max(pos) + 1, batch)} max|dlogit| {err:.3e} torch {err_torch:.3e} "
+          f"bound {bound:.3e}", flush=True)
+    assert err <= bound
+    check_tokens(toks, ref_toks, ref_logits, bound)
+    check_kv(h)
+    h.close()
+
+
 def test_host_staged_rows_match_device_rows():
     """``decode_rows_host`` (pinned host staging, the engine's batch path) gives the
     same tokens and the same KV writes, bit for bit, as ``decode_rows`` on device

@@ -106,13 +106,19 @@ def test_buckets_and_auto_splits():
 @pytest.mark.parametrize("batch", [1, 2, 4, 8])
 @pytest.mark.parametrize("splits", [1, 2, 4, 8, 16])
 def test_tagged_exchange_preconditions_at_256_cus(batch, splits):
-    """Even GEMV row blocks of <= 32 rows, one query head per attention task and
-    an LM task on every workgroup; the per-KV-head schedule is rejected."""
+    """Even GEMV row blocks of <= 32 rows and an LM task on every workgroup, with
+    attention tasks of one query head (flagged) or of both heads of a KV head."""
     from nanovllm.backends.megakernel.taskgraph import _check_tagged_preconditions
-    for groups in (1, 4):
-        _check_tagged_preconditions(build_segments(batch, splits, 256, 28, groups, q_head_tasks=True))
-    with pytest.raises(RuntimeError, match="one query head"):
-        _check_tagged_preconditions(build_segments(batch, splits, 256, 28, 1))
+    for pair in (False, True):
+        for groups in (1, 4):
+            segs = build_segments(batch, splits, 256, 28, groups, q_head_tasks=True, pair_heads=pair)
+            _check_tagged_preconditions(segs)
+            attn = [t for seg in segs for st in seg.stages if st.op == native.OP_ATTN for t in st.tasks]
+            # every (row, KV head, split, query head) exactly once per layer
+            assert len(attn) == 28 * batch * 8 * splits * (1 if pair else 2)
+            heads = {(t.a0 & native.ATTN_QHEAD) // native.ATTN_QHEAD for t in attn}
+            assert all(bool(t.a0 & native.ATTN_ONE_HEAD) != pair for t in attn)
+            assert heads == ({0} if pair else {0, 1})
 
 
 def test_tagged_exchange_needs_one_norm_task_per_workgroup_per_layer():
@@ -218,3 +224,20 @@ def test_tagged_split_rule():
     assert [t(c, batch=2) for c in (64, 65, 480, 1000, 2048)] == [1, 2, 8, 8, 8]
     assert [t(c, batch=8) for c in (200, 300, 2048)] == [1, 2, 2] and t(2048, batch=4) == 4
     assert t(100, minimum=4) == 4 and t(2048, minimum=16, batch=8) == 16
+
+
+def test_pair_head_rule_and_its_split_rule():
+    """Tasks of both query heads from batch 4 at contexts of two pages or more;
+    their split rule aims at 256 positions per split, capped at 32 // batch (16)."""
+    from nanovllm.backends.megakernel.schedule import tagged_attn_splits as t, tagged_pair_heads as p
+
+    assert [p(b, 2000) for b in (1, 2, 4, 8)] == [False, False, True, True]
+    assert [p(8, c) for c in (1, 256, 257, 2048)] == [False, False, True, True]
+    assert [t(c, batch=8, pair_heads=True) for c in (200, 300, 700, 1100, 2048)] == [1, 2, 4, 4, 4]
+    assert [t(c, batch=4, pair_heads=True) for c in (300, 1100, 2048)] == [2, 8, 8]
+    assert t(2048, batch=1, pair_heads=True) == 8 and t(10 ** 5, batch=1, pair_heads=True) == 16
+    assert t(100, minimum=8, batch=8, pair_heads=True) == 8
+    # a stage of pair tasks at the cap fills the 256 workgroups exactly once
+    for b in (4, 8):
+        splits = t(10 ** 5, batch=b, pair_heads=True)
+        assert b * 8 * splits == 256

@@ -22,7 +22,6 @@ def _run_noalloc(h: Harness, ids, pos, tables):
     """One step through the allocation-free entry point with the decoder's own
     schedule and row buffers; returns (tokens, logits, status)."""
     from nanovllm.backends.megakernel import native
-    from nanovllm.backends.megakernel.schedule import batch_bucket
 
     dec = h.dec
     rows = len(ids)
@@ -31,7 +30,7 @@ def _run_noalloc(h: Harness, ids, pos, tables):
                    torch.tensor(pos, dtype=torch.int64, device="cuda"),
                    torch.tensor([list(t) + [0] * (width - len(t)) for t in tables], dtype=torch.int32,
                                 device="cuda"))
-    geo = dec._geometry(batch_bucket(rows), dec.splits_for(width * dec.block_size, rows))
+    geo = dec.geometry_for(width * dec.block_size, rows)
     logits = torch.zeros(rows, VOCAB, dtype=torch.bfloat16, device="cuda")
     out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
     status = torch.full((1,), -7, dtype=torch.int32, device="cuda")
