@@ -538,6 +538,103 @@ __device__ __forceinline__ void chunk_mfma(const uint8_t* slot, const uint4* x4,
     if (n < RPC && kg == 0) part[(size_t)(wave * 32 + n) * B] = acc[0];
   }
 }
+// x[lane] + x[lane ^ 32] and x[lane] + x[lane ^ 16] on every lane (gfx950
+// permlane swaps: one VALU op instead of an LDS crossbar round trip).
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// MFMA GEMV of one chunk at batch 4 and 8 on the 4x4x4 block MFMA (16 blocks
+// of 4 x 4 x 4 per instruction): a block is an 8-element K piece (two
+// instructions, its low and high halves), A its 4 batch rows of x, B its 4
+// weight rows, so every operand byte read from LDS is used (the 16x16x32 form
+// reads the chunk's few weight rows and the batch rows many times over:
+// measured LDS-bound at batch 8). Wave w takes K quarter w in 128-element steps
+// (lane 4 blk + i: piece blk of the step, batch row 4 h + i of x, weight row
+// 4 g + i), the 16 blocks' sums are added across lanes, and lanes 0-3 write
+// part[(w * 32 + row) * B + b] as chunk_mfma does. Rows past the chunk's
+// (K = 3072: 2 of a group's 4) repeat its rows and are not written.
+template <int B, int K>
+__device__ __forceinline__ void chunk_mfma4(const uint8_t* slot, const uint4* x4, float* part) {
+  static_assert(B == 4 || B == 8, "4x4x4 GEMV for batch 4 and 8");
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  constexpr int RPC = K == 1024 ? 8 : (K == 2048 ? 4 : 2);
+  constexpr int NG = RPC >= 4 ? RPC / 4 : 1;  // groups of 4 weight rows
+  constexpr int NH = B / 4;                   // groups of 4 batch rows
+  constexpr int STEPS = K / 4 / 128;          // 128-element steps of the wave's K quarter
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int blk = lane >> 2, i = lane & 3;
+  p4_f32x4 acc[NG][NH];
+#pragma unroll
+  for (int g = 0; g < NG; g++)
+#pragma unroll
+    for (int h = 0; h < NH; h++) acc[g][h] = p4_f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint4* wrow[NG];
+#pragma unroll
+  for (int g = 0; g < NG; g++) wrow[g] = reinterpret_cast<const uint4*>(slot + (size_t)((4 * g + i) & (RPC - 1)) * (K * 2));
+#pragma unroll
+  for (int s = 0; s < STEPS; s++) {
+    const int q = (K / 32) * wave + 16 * s + blk;  // 16-byte piece of the row
+    uint4 wv[NG], xv[NH];
+#pragma unroll
+    for (int g = 0; g < NG; g++) wv[g] = wrow[g][wpiece((4 * g + i) & (RPC - 1), q)];
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      const int b = 4 * h + i;
+      xv[h] = x4[(size_t)b * (K == 1024 ? XS_H / 8 : K / 8) + (K == 1024 ? q : xs_piece(b, q))];
+    }
+#pragma unroll
+    for (int g = 0; g < NG; g++)
+#pragma unroll
+      for (int h = 0; h < NH; h++) {
+        const uint2 wl = make_uint2(wv[g].x, wv[g].y), wh = make_uint2(wv[g].z, wv[g].w);
+        const uint2 xl = make_uint2(xv[h].x, xv[h].y), xh = make_uint2(xv[h].z, xv[h].w);
+        acc[g][h] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4, xl), __builtin_bit_cast(s16x4, wl),
+                                                           acc[g][h], 0, 0, 0);
+        acc[g][h] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4, xh), __builtin_bit_cast(s16x4, wh),
+                                                           acc[g][h], 0, 0, 0);
+      }
+  }
+  // sum over the 16 blocks: lanes i, i + 4, ..., i + 60 (rotations by 4 and 8
+  // within each row of 16 lanes, then across the rows)
+#pragma unroll
+  for (int g = 0; g < NG; g++)
+#pragma unroll
+    for (int h = 0; h < NH; h++)
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        float v = acc[g][h][m];
+        v += dpp_mov<0x124>(v, 0.f);  // row_ror:4
+        v += dpp_mov<0x128>(v, 0.f);  // row_ror:8
+        acc[g][h][m] = xor32_sum(xor16_sum(v));
+      }
+  if (lane < 4) {
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+      const int row = 4 * g + lane;
+      if (row < RPC) {
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+          *reinterpret_cast<float4*>(part + (size_t)(wave * 32 + row) * B + 4 * h) =
+              make_float4(acc[g][h][0], acc[g][h][1], acc[g][h][2], acc[g][h][3]);
+      }
+    }
+  }
+}
+// GEMV chunks on chunk_mfma4: K = 2048 and 3072 (o_proj, down: 4 and 2 rows
+// per chunk) at batch 4 and 8. Measured per chunk at batch 8: down 1.06 ->
+// 0.86 us, o_proj 0.80 -> 0.65 us; but K = 1024 (8 rows per chunk, where the
+// 16x16x32 form wastes less) 0.5 -> 0.9 us, its block sums costing more than
+// the operand reads saved. Step: batch 4 693 -> 662 us, C5 batch 4 912 -> 868 us.
+template <int B, int K>
+constexpr bool p4_mfma4() {
+  return B >= 4 && K >= 2048;
+}
 // Chunk-result sink of the MFMA GEMV (p4_chunks passes it the chunk's rows).
 struct PartSink {
   float* part;
@@ -755,7 +852,10 @@ __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int ro
     if (ct != nullptr && threadIdx.x == 0) ct[0] = wall_clock64();
 #endif
     if constexpr (std::is_same<Out, PartSink>::value) {
-      if (!aborted) chunk_mfma<B, K>(slot, xsrc.x4, out.part + (size_t)j * RPC * B);
+      if (!aborted) {
+        if constexpr (p4_mfma4<B, K>()) chunk_mfma4<B, K>(slot, xsrc.x4, out.part + (size_t)j * RPC * B);
+        else chunk_mfma<B, K>(slot, xsrc.x4, out.part + (size_t)j * RPC * B);
+      }
     } else if constexpr (std::is_same<Out, LmSink>::value) {
       // (every wave still takes each hand-over barrier above)
       const int wave = threadIdx.x >> 6, r = (threadIdx.x & 15) & 7;
@@ -1031,19 +1131,8 @@ __device__ __forceinline__ bool p4_lm_finish(const MkdStepDesc& d, const P4& c, 
   return true;
 }
 
-// x[lane] + x[lane ^ 32] and x[lane] + x[lane ^ 16] on every lane (gfx950
-// permlane swaps: one VALU op instead of an LDS crossbar round trip).
-__device__ __forceinline__ float xor32_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float xor16_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // Positions of one ATTN task: split `split` of `nsplit` covers [p_begin, p_end)
-// of the row's pos + 1 positions (splits of a multiple of 64 positions); the
+// of the row's pos + 1 positions (whole KV chunks but the last split's end); the
 // cached ones, [p_begin, c_end), come in KV chunks of 32 positions that the DMA
 // waves stage in the LDS ring; the token's own position (pos) is not in the
 // cache yet and comes from this step's k and v. Computed identically by the
