@@ -45,6 +45,11 @@ def step_bytes(contexts: list[int]) -> int:
     return WEIGHT_BYTES + sum(KV_BYTES_PER_POS * c + KV_BYTES_PER_POS + EMBED_ROW_BYTES for c in contexts)
 
 
+def progress(what: str) -> None:
+    """One line on stderr per phase (a long default run shows it is alive)."""
+    print(f"bench: {what}", file=sys.stderr, flush=True)
+
+
 def build_decoder(num_layers=28, num_blocks=64, launch="persistent", variant="tagged", fusion_groups=1,
                   attn_splits=1, **options):
     import torch
@@ -502,6 +507,7 @@ def main():
                      "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(avg_launch_ms * 1e3, 2)},
     }
     if not args.no_sweep:
+        progress("sweep: batch 1-8 short context")
         sweep = {}
         for mode in ("persistent", "graph"):
             for b in (1, 2, 4, 8):
@@ -511,8 +517,12 @@ def main():
                                          "GBps": round(sum(step_bytes(c) for c in ctxs) / len(ctxs) / us / 1e3, 1)}
         result["sweep"] = sweep
         # C5 (prompt lengths U[1024,1920], ragged tables): the same boundary at long context
+        progress("sweep: C5 long contexts")
         result["sweep_long_c5"] = long_context_runs("c5", 32, 4, dec=dec)
+        progress("sweep: C4")
+        result["sweep_long_c4"] = long_context_runs("c4", 32, 4, dec=dec)
     if not args.no_cpu_baseline:
+        progress("cpu baseline")
         result["cpu_baseline"] = cpu_baseline()
     dec.close()
     print(json.dumps(result))
