@@ -203,8 +203,6 @@ __device__ __forceinline__ void poll_issue(Addr addr, uint64_t (&a)[N]) {
 template <int N, class Addr>
 __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_t (&v)[N], uint32_t tag,
                                             const Ws& ws) {
-  static_assert(N <= 32, "pending mask");
-  uint32_t pending = N == 32 ? ~0u : ((1u << N) - 1u);
   // The device error word and the clock are read only by a poll that has
   // already spun 62 rounds: the error word is loaded ahead of a round's polls
   // and examined with their results, so no round waits for a load of its own
@@ -212,14 +210,20 @@ __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_
   uint32_t err = 0u;
   uint64_t t0 = 0;
   for (uint32_t spin = 0;; spin++) {
-    // Every word is examined on every round (one already seen keeps its value
-    // and tag in a[k]): a load the compiler sees unconsumed on some path makes
-    // it wait for all of the wave's memory operations before that register is
-    // next written, wherever that is.
+    // A lane re-polls all of its words until one round finds every tag
+    // current (a word once current stays so until this task is done: its
+    // next writer depends on this task's outputs). Per-word pending masks
+    // cost a branch per word and, inlined at every poll site, put the
+    // batch-8 kernel over the instruction cache (batch 8 -29 us, C4 -34 us,
+    // measured without them). Every word is examined on every round: a load
+    // the compiler sees unconsumed on some path makes it wait for all of the
+    // wave's memory operations before that register is next written.
+    bool all = true;
 #pragma unroll
-    for (int k = 0; k < N; k++)
-      if (tw_tag(a[k]) == tag) { v[k] = a[k]; pending &= ~(1u << k); }
-    if (pending == 0u) {
+    for (int k = 0; k < N; k++) all = all && tw_tag(a[k]) == tag;
+    if (all) {
+#pragma unroll
+      for (int k = 0; k < N; k++) v[k] = a[k];
       asm volatile("" ::"v"(err));  // (loaded before the polls just examined)
       return true;
     }
@@ -235,8 +239,7 @@ __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_
     __builtin_amdgcn_s_sleep(1);  // (longer pauses measured slower at every batch size)
     if ((spin & 63u) == 62u) err = ld_co(ws.line(CTR_ERR));
 #pragma unroll
-    for (int k = 0; k < N; k++)
-      if ((pending >> k) & 1u) a[k] = ld_co(addr(k));
+    for (int k = 0; k < N; k++) a[k] = ld_co(addr(k));
   }
 }
 // Load N tagged words (addr(k), k < N) and spin until each carries `tag`.
@@ -789,27 +792,62 @@ __device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, c
   const int layer = w.layer;
   const uint32_t tag = p4_tag(c.epoch, layer);
   const int t = p4_tid();
-  switch (w.op) {
-    // (the residual after QKV is consumed by the gate/up prologue of the same
-    // layer: published only when that prologue runs in a later launch)
-    case MKD_OP_QKV: {
-      const uint16_t* nw = p4_wptr(d, layer, MKD_W_LN_IN);
-      const ResRange r = p4_res_range<QKV_N / 256>(w);
-      const int rn = (w.a2 & QKV_PUBLISH_RES) ? r.n : 0;
-      if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, r.first, rn, rk);
-      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, r.first, rn, rk);
+  (void)t;
+  if constexpr (B < 4) {
+    // batch 1-2: one inlined p4_stage_norm per call site (the code fits the
+    // instruction cache; shared, it measured slower at batch 1)
+    switch (w.op) {
+      case MKD_OP_QKV: {
+        const uint16_t* nw = p4_wptr(d, layer, MKD_W_LN_IN);
+        const ResRange r = p4_res_range<QKV_N / 256>(w);
+        const int rn = (w.a2 & QKV_PUBLISH_RES) ? r.n : 0;
+        if (layer == 0) return p4_stage_norm<B>(d, c, true, 0, 0, 0, nw, r.first, rn, rk);
+        return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, layer - 1), nw, r.first, rn, rk);
+      }
+      case MKD_OP_GATEUP: {
+        const ResRange r = p4_res_range<I / 256>(w);
+        return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST), r.first,
+                                (w.a2 & GATEUP_PUBLISH_RES) ? r.n : 0, rk);
+      }
+      case MKD_OP_OPROJ: return p4_stage_copy<B, QS>(c, TW_ATTN, tag);
+      case MKD_OP_DOWN: return p4_stage_copy<B, I>(c, TW_ACT, tag);
+      case MKD_OP_LMHEAD:
+        return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, d.num_layers - 1), d.final_norm, 0, 0, rk);
+      default: return true;
     }
-    case MKD_OP_GATEUP: {
-      const ResRange r = p4_res_range<I / 256>(w);
-      return p4_stage_norm<B>(d, c, false, TW_O, TW_RES1, tag, p4_wptr(d, layer, MKD_W_LN_POST), r.first,
-                              (w.a2 & GATEUP_PUBLISH_RES) ? r.n : 0, rk);
-    }
-    case MKD_OP_OPROJ: return p4_stage_copy<B, QS>(c, TW_ATTN, tag);
-    case MKD_OP_DOWN: return p4_stage_copy<B, I>(c, TW_ACT, tag);
-    case MKD_OP_LMHEAD:
-      return p4_stage_norm<B>(d, c, false, TW_DOWN, TW_RES2, p4_tag(c.epoch, d.num_layers - 1), d.final_norm, 0, 0, rk);
-    default: return true;
   }
+  if (w.op == MKD_OP_OPROJ) return p4_stage_copy<B, QS>(c, TW_ATTN, tag);
+  if (w.op == MKD_OP_DOWN) return p4_stage_copy<B, I>(c, TW_ACT, tag);
+  if (w.op != MKD_OP_QKV && w.op != MKD_OP_GATEUP && w.op != MKD_OP_LMHEAD) return true;
+  // batch 4-8: the three RMSNorm prologues share one inlined copy of
+  // p4_stage_norm, their operands selected here (a copy per call site would
+  // triple its code: the batch-8 kernel was over the instruction cache)
+  // (the residual after QKV is consumed by the gate/up prologue of the same
+  // layer: published only when that prologue runs in a later launch)
+  bool from_embed = false;
+  size_t hid = TW_DOWN, resid = TW_RES2;
+  uint32_t tag_in = tag;
+  const uint16_t* nw;
+  int res_first = 0, res_n = 0;
+  if (w.op == MKD_OP_QKV) {
+    nw = p4_wptr(d, layer, MKD_W_LN_IN);
+    const ResRange r = p4_res_range<QKV_N / 256>(w);
+    res_first = r.first;
+    res_n = (w.a2 & QKV_PUBLISH_RES) ? r.n : 0;
+    from_embed = layer == 0;
+    tag_in = p4_tag(c.epoch, layer - 1);
+  } else if (w.op == MKD_OP_GATEUP) {
+    nw = p4_wptr(d, layer, MKD_W_LN_POST);
+    const ResRange r = p4_res_range<I / 256>(w);
+    res_first = r.first;
+    res_n = (w.a2 & GATEUP_PUBLISH_RES) ? r.n : 0;
+    hid = TW_O;
+    resid = TW_RES1;
+  } else {
+    nw = d.final_norm;
+    tag_in = p4_tag(c.epoch, d.num_layers - 1);
+  }
+  return p4_stage_norm<B>(d, c, from_embed, hid, resid, tag_in, nw, res_first, res_n, rk);
 }
 
 // Chunks are handed from the DMA waves to the compute waves in groups of G
