@@ -109,6 +109,13 @@ __device__ __forceinline__ bool lm_better(float v, int i, float bv, int bi) {
   const bool vn = v != v, bn = bv != bv;
   return vn ? (!bn || i < bi) : (!bn && (v > bv || (v == bv && i < bi)));
 }
+// The same rule for a running argmax that visits rows in increasing order: a
+// later row never wins a tie, so only a larger value or a first NaN replaces
+// the best (an all -inf run keeps the "no candidate" index, which the final
+// merge turns into token 0, as torch.argmax of all -inf gives).
+__device__ __forceinline__ bool lm_later_better(float v, float bv) {
+  return v != v ? bv == bv : v > bv;
+}
 
 // a.lo*b.lo + a.hi*b.hi + c in fp32 (v_dot2_f32_bf16).
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {

@@ -276,13 +276,7 @@ template <int B, int K>
 __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t tag) {
   constexpr int PER = B * (K / 2) / 256;  // words per thread
   // (batch 8, down: 12-word groups, four rounds instead of six)
-#ifndef MKD_NB8_QS
-#define MKD_NB8_QS 8
-#endif
-#ifndef MKD_NB8_I
-#define MKD_NB8_I 12
-#endif
-  constexpr int NB = B >= 8 && K == 3072 ? MKD_NB8_I : (B >= 8 && K == QS ? MKD_NB8_QS : largest_divisor_le8(PER));
+  constexpr int NB = B >= 8 && K == 3072 ? 12 : largest_divisor_le8(PER);
   static_assert(PER % NB == 0, "whole groups");
   const int t = p4_tid();
   const uint64_t* src = c.ws.tw(base + (size_t)c.rep * TW_GROUP);
@@ -687,7 +681,7 @@ __device__ __forceinline__ void chunk_lm_mfma(const uint8_t* slot, const uint4* 
   for (int i = 0; i < 4; i++) {
     const float acc = a0[i] + a1[i];
     const float v = valid ? round_bf(acc) : -INFINITY;
-    const bool better = lm_better(v, row, lb.v[i], lb.i[i]);
+    const bool better = lm_later_better(v, lb.v[i]);  // (this lane's rows come in increasing order)
     lb.v[i] = better ? v : lb.v[i];
     lb.i[i] = better ? row : lb.i[i];
     const int b = 4 * kg + i;
@@ -991,7 +985,7 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
 #pragma unroll
         for (int b = 0; b < B; b++) {
           const float v = round_bf(acc[b]);
-          const bool better = lm_better(v, row, best.v[b], best.i[b]);
+          const bool better = lm_later_better(v, best.v[b]);  // (rows in increasing order)
           best.v[b] = better ? v : best.v[b];
           best.i[b] = better ? row : best.i[b];
         }
