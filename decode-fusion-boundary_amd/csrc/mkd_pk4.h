@@ -852,7 +852,13 @@ __device__ __forceinline__ bool p4_prologue(const MkdStepDesc& d, const P4& c, c
 // hold group g + 1 in the remaining slots.
 template <int NS>
 struct P4G {
-  static constexpr int G = NS / 2 < 4 ? NS / 2 : 4;
+  // Groups of 2 (measured against min(NS / 2, 4), i.e. 4 at batch 1-4 and 3 at
+  // batch 8): a smaller group lets the DMA waves refill sooner, keeping more
+  // chunks in flight while the compute waves work (batch 1 499 -> 482 us,
+  // batch 8 858 -> 835, C5 batch 8 1161 -> 1105); groups of 1 (a barrier per
+  // chunk) were slower at batch 2-8.
+  static constexpr int G = 2;
+  static_assert(2 * G <= NS, "two groups fit the ring");
 };
 
 // The chunk loop of one GEMV task (the op is fixed for the whole loop).
