@@ -1178,14 +1178,37 @@ __device__ __forceinline__ bool p4_lm_finish(const MkdStepDesc& d, const P4& c, 
 constexpr int KV_CHUNK = 32;  // positions per KV chunk: 32 K rows (8 KiB) + 32 V rows (8 KiB)
 struct AttnGeo {
   int pos, p_begin, p_end, c_end, nch;
+  int ns;     // splits this row uses (<= the schedule's): the last of them merges
   bool live;  // a row of this step with a valid position
 };
+// Fewest KV chunks per split: the schedule's split count is sized for the
+// longest context of the prepared steps or from the block table's width
+// (whole pages); a row's context in this step may need fewer. A split past
+// the row's count has no positions and does nothing, and split ns - 1 merges
+// (batch 2, contexts 1-65 scheduled with 2 splits: 594 -> 552 us per step).
+template <int B>
+constexpr int p4_split_min_chunks() {
+  // batch 2 only (0: none). Batch 1's host rule already fits short contexts
+  // (one split below ~170 positions) and batch 4-8 take one split below two
+  // pages; there the added code alone measured +4 to +5 us.
+  return B == 2 ? 2 : 0;
+}
 __device__ __forceinline__ AttnGeo attn_geo(int rows, int b, int pos_in, int page_stride, int bs, int split,
-                                            int nsplit) {
+                                            int nsplit, int min_chunks) {
   AttnGeo g;
   g.live = b < rows && pos_in >= 0 && pos_in < MKD_MAX_POSITION && pos_in / bs < page_stride;
   g.pos = g.live ? pos_in : 0;
   const int ctx = g.pos + 1;
+  g.ns = nsplit;
+  if (min_chunks > 0) {
+    nsplit = max(1, min(nsplit, ((ctx + KV_CHUNK - 1) / KV_CHUNK + min_chunks - 1) / min_chunks));
+    g.ns = nsplit;
+    if (split >= nsplit) {  // no positions for this split
+      g.p_begin = g.p_end = g.c_end = ctx;
+      g.nch = 0;
+      return g;
+    }
+  }
   // the row's KV_CHUNK-position chunks dealt out evenly, the first nck % nsplit
   // splits taking one more (measured against equal spans rounded up to 64
   // positions: C4 batch 8 1057 -> 1029 us, C5 batch 8 1220 -> 1202 us; moving
@@ -1235,10 +1258,11 @@ __device__ __forceinline__ void p4_skip_chunks(int cc, int nch) {
     if ((cc + j) % P4G<NS>::G == 0) raw_barrier();
 }
 // KV chunk count of an ATTN task (as the DMA waves compute it).
+template <int B>
 __device__ __forceinline__ int p4_attn_chunks(const MkdStepDesc& d, const Inst& w) {
   const int b = (w.a0 & 63) / NKV;  // (a0 = b * 8 + h plus query-head flags from bit 6)
   const int pos_in = b < d.rows ? as_const(d.cache_seqlens)[b] : 0;
-  return attn_geo(d.rows, b, pos_in, d.page_stride, d.block_size, w.a1, w.a2).nch;
+  return attn_geo(d.rows, b, pos_in, d.page_stride, d.block_size, w.a1, w.a2, p4_split_min_chunks<B>()).nch;
 }
 
 // Softmax in base 2: scores scaled by hd^-0.5 * log2(e), so that every
@@ -1325,9 +1349,13 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   const int b = bh / NKV, h = bh % NKV, qh = GROUP * h + g;  // (PAIR: qh and qh + 1)
   const int bs = d.block_size;
   const int pos_in = b < d.rows ? as_const(d.cache_seqlens)[b] : 0;
-  const AttnGeo ag = attn_geo(d.rows, b, pos_in, d.page_stride, bs, split, nsplit);
+  const AttnGeo ag = attn_geo(d.rows, b, pos_in, d.page_stride, bs, split, nsplit, p4_split_min_chunks<B>());
   nch = ag.nch;
   if (b < d.rows && !ag.live && t == 0) st_co(c.ws.line(CTR_ERR), ERR_BAD_INPUT);
+  if constexpr (p4_split_min_chunks<B>() > 0) {
+    if (split >= ag.ns) return true;  // a split this row does not use (wave-uniform: no barrier)
+    nsplit = ag.ns;
+  }
   const int pos = ag.pos, p_begin = ag.p_begin, p_end = ag.p_end, c_end = ag.c_end;
   const bool active = ag.live && as_const(d.row_active)[b] != 0;
   const bool writes_kv = g == 0 && split == 0 && active;  // one task stores the new token's K/V
@@ -1685,6 +1713,7 @@ __device__ __forceinline__ T karg_field(const uint8_t* karg, size_t off) {
   typedef __attribute__((address_space(4))) const T ct;
   return *reinterpret_cast<ct*>(reinterpret_cast<uintptr_t>(karg) + off);
 }
+template <int B>
 __device__ __forceinline__ void dma_decode_attn(DmaTask& t, const uint8_t* karg, const Inst& w) {
   const int b = (w.a0 & (ATTN_QHEAD - 1)) / NKV, h = w.a0 % NKV;
   const int rows = karg_field<int32_t>(karg, offsetof(MkdStepDesc, rows));
@@ -1692,7 +1721,7 @@ __device__ __forceinline__ void dma_decode_attn(DmaTask& t, const uint8_t* karg,
   const int stride = karg_field<int32_t>(karg, offsetof(MkdStepDesc, page_stride));
   const int32_t* seqlens = karg_field<int32_t*>(karg, offsetof(MkdStepDesc, cache_seqlens));
   const int pos_in = b < rows ? as_const(seqlens)[b] : 0;
-  const AttnGeo g = attn_geo(rows, b, pos_in, stride, bs, w.a1, w.a2);
+  const AttnGeo g = attn_geo(rows, b, pos_in, stride, bs, w.a1, w.a2, p4_split_min_chunks<B>());
   t.kind = 3;
   t.nch = g.nch;
   if (g.nch == 0) return;
@@ -1733,6 +1762,7 @@ __device__ __forceinline__ void dma_issue_attn(const DmaTask& t, int j, uint8_t*
   }
 }
 
+template <int B>
 __device__ __forceinline__ DmaTask dma_decode(cuint64_t* lp, const uint16_t* emb, const uint8_t* karg, const Inst& w,
                                               int dw) {
   auto W = [&](int which) { return reinterpret_cast<const uint16_t*>(lp[w.layer * MKD_LAYER_PTRS + which]); };
@@ -1741,7 +1771,7 @@ __device__ __forceinline__ DmaTask dma_decode(cuint64_t* lp, const uint16_t* emb
   t.b1 = nullptr;
   switch (w.op) {
     case MKD_OP_ATTN:
-      dma_decode_attn(t, karg, w);
+      dma_decode_attn<B>(t, karg, w);
       return t;
     case MKD_OP_QKV:
       t.b0 = a0 < QS ? W(MKD_W_Q) + (size_t)a0 * H
@@ -1874,7 +1904,7 @@ __device__ __noinline__ void p4_dma(const uint64_t* layer_ptrs, const uint16_t* 
       const Inst w = pinst;
       pf++;
       if (pf < n) pinst = load_inst(crow + pf * MKD_INST_WORDS);
-      const DmaTask t = dma_decode(lp, emb, karg, w, dw);
+      const DmaTask t = dma_decode<B>(lp, emb, karg, w, dw);
       if (t.nch > 0) return t;
     }
     DmaTask none{};
@@ -1993,7 +2023,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
           aborted = !p4_attn<B, Cfg::NS, false>(d, c, w.layer, w.a0, w.a1, w.a2, tr, ring, cc, nkv);
         }
       } else {
-        nkv = p4_attn_chunks(d, w);
+        nkv = p4_attn_chunks<B>(d, w);
         p4_skip_chunks<Cfg::NS>(cc, nkv);
       }
       cc += nkv;
