@@ -1336,9 +1336,7 @@ __device__ __forceinline__ void p4_fold_splits(const Ws ws, size_t pbase, int ns
 }
 constexpr int ATTN_QHEAD = 64, ATTN_ONE_HEAD = 128;
 constexpr int P4_PAIR_MIN_B = 4;  // smallest batch whose kernel runs tasks of both query heads
-#ifndef MKD_B1_FOLD_SPR
-#define MKD_B1_FOLD_SPR 3
-#endif  // task word a0 flags (b * 8 + h < 64)
+  // task word a0 flags (b * 8 + h < 64)
 template <int B, int NS, bool PAIR>
 __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int a0, int split, int nsplit,
                                         uint64_t* tr, uint8_t* ring, int cc, int& nch) {
@@ -1579,7 +1577,9 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     // splits' partials here, up to SPR splits per poll round (all of a round's
     // loads in flight at once: one round trip instead of one per split), in
     // split order
-    constexpr int SPR = MKD_B1_FOLD_SPR;
+    // (8 partials per round at batch 1 and 4: C5 batch 1 643 -> 614 us, C5 batch
+    // 4 834 -> 808 than 3 per round, but batch 8 +14 us; 15 per round spills)
+    constexpr int SPR = B == 8 ? 3 : 8;
     for (int sp0 = 0; nsplit > 1 && sp0 < nsplit - 1; sp0 += SPR) {
       uint64_t e[3 * SPR];
       // (entries past the last split repeat its words)
