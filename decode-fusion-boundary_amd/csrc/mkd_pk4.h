@@ -1334,9 +1334,8 @@ __device__ __forceinline__ void p4_fold_splits(const Ws ws, size_t pbase, int ns
     }
   }
 }
-constexpr int ATTN_QHEAD = 64, ATTN_ONE_HEAD = 128;
+constexpr int ATTN_QHEAD = 64, ATTN_ONE_HEAD = 128;  // task word a0 flags (b * 8 + h < 64)
 constexpr int P4_PAIR_MIN_B = 4;  // smallest batch whose kernel runs tasks of both query heads
-  // task word a0 flags (b * 8 + h < 64)
 template <int B, int NS, bool PAIR>
 __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int layer, int a0, int split, int nsplit,
                                         uint64_t* tr, uint8_t* ring, int cc, int& nch) {
