@@ -1147,11 +1147,22 @@ __device__ __forceinline__ bool p4_lm_finish(const MkdStepDesc& d, const P4& c, 
   bool ok = true;
   for (int b = wave; b < d.rows; b += PK_CW) {
     float v = -INFINITY; int i = 0x7fffffff;
-    for (int s = lane; s < d.lm_slots; s += 64) {
-      uint64_t e[2];
-      ok = ok && poll_tagged<2>([&](int k) { return c.ws.tw(TW_LM + ((size_t)s * MAXB + b) * 2 + k); }, e, tag, c.ws);
-      const float v2 = __uint_as_float((uint32_t)e[0]); const int i2 = (int)(uint32_t)e[1];
-      if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
+    // four slots per lane and poll round (slots lane, lane + 64, ...; one round
+    // for the usual 256 slots instead of four back to back); past the slot
+    // count a lane re-reads its first slot, which changes no (max, first index)
+    for (int s0 = lane; s0 < d.lm_slots; s0 += 256) {
+      uint64_t e[8];
+      ok = ok && poll_tagged<8>(
+                     [&](int k) {
+                       const int s = s0 + 64 * (k >> 1) < d.lm_slots ? s0 + 64 * (k >> 1) : s0;
+                       return c.ws.tw(TW_LM + ((size_t)s * MAXB + b) * 2 + (k & 1));
+                     },
+                     e, tag, c.ws);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float v2 = __uint_as_float((uint32_t)e[2 * q]); const int i2 = (int)(uint32_t)e[2 * q + 1];
+        if (lm_better(v2, i2, v, i)) { v = v2; i = i2; }
+      }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
