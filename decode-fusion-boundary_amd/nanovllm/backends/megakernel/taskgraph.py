@@ -542,7 +542,9 @@ class TaskGraphDecoder:
         if self._mask_dirty:
             self._row_active.fill_(1)
             self._mask_dirty = False
-        geo = self.geometry_for(cols * self.block_size, 1)
+        # (the split rule sees the row's real context, known here; the block
+        # table's width overstates it by up to a page)
+        geo = self.geometry_for(int(position) + 1, 1)
         self._launch(self._desc_for(1, geo), geo)
         return int(self._read_status(1)[0])
 
@@ -578,7 +580,7 @@ class TaskGraphDecoder:
         if self._mask_dirty:
             self._row_active.fill_(1)
             self._mask_dirty = False
-        geo = self.geometry_for(cols * self.block_size, rows)
+        geo = self.geometry_for(max(int(p) for p in positions) + 1, rows)  # (real contexts, as decode_row)
         self._launch(self._desc_for(rows, geo), geo)
         return self._read_status(rows)
 
