@@ -1005,6 +1005,16 @@ __device__ __forceinline__ void p4_task_chunks(const MkdStepDesc& d, const P4& c
 }
 
 constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
+// Replicas of the all-read tagged words this batch's kernel writes (the
+// workspace holds TW_NREP); workgroups on XCD x read replica x % p4_nrep.
+// Measured per batch (us per step with 8 / 4 / 2 / 1 replicas): batch 1 479 /
+// 481 / 492 / 516; batch 8 831 / 800 / 802 / 813 (C4 945 / 912, C5 1102 /
+// 1072): at batch 4-8 the replica stores cost more than spreading the reads
+// over 8 copies saves.
+template <int B>
+constexpr int p4_nrep() {
+  return B >= 4 ? 4 : TW_NREP;
+}
 
 // The residual words this task's owner threads staged in its prologue: one
 // store per (word, replica), at most one per thread (at most 2 owners x 8 rows
@@ -1021,13 +1031,13 @@ __device__ __forceinline__ ResWord p4_residual_word(const P4& c, const Inst& w, 
   const ResRange r = p4_res_range<F>(w);
   const uint32_t* stage = c.stage + c.par * P4_STAGE_WORDS;
   const int t = p4_tid();
-  constexpr int LR = ilog2(TW_NREP), LB = ilog2(B);
-  static_assert(2 * B * 2 * TW_NREP <= PK_CW * 64, "one residual store per thread");
+  constexpr int LR = ilog2(p4_nrep<B>()), LB = ilog2(B);
+  static_assert(2 * B * 2 * p4_nrep<B>() <= PK_CW * 64, "one residual store per thread");
   const int e = (t & 63) * PK_CW + (t >> 6);
   if (e >= (r.n << (LB + 1 + LR))) return ResWord{nullptr, 0};
   const int k = e >> LR, o = k >> (LB + 1), b = (k >> 1) & (B - 1);
   const size_t word = base + (size_t)b * (H / 2) + 2 * (r.first + o) + (k & 1);
-  return ResWord{c.ws.tw(word + (size_t)(e & (TW_NREP - 1)) * TW_GROUP), tw_make(stage[k], tag)};
+  return ResWord{c.ws.tw(word + (size_t)(e & (p4_nrep<B>() - 1)) * TW_GROUP), tw_make(stage[k], tag)};
 }
 
 // Publish one GEMV task's rows as tagged bf16 pairs. Entry e = (pair i, row b,
@@ -1037,7 +1047,7 @@ __device__ __forceinline__ ResWord p4_residual_word(const P4& c, const Inst& w, 
 // single wave costs several cycles.
 template <int B, int OP>
 __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
-  constexpr int LR = OP == MKD_OP_QKV ? 0 : ilog2(TW_NREP);  // QKV words have one reader XCD
+  constexpr int LR = OP == MKD_OP_QKV ? 0 : ilog2(p4_nrep<B>());  // QKV words have one reader XCD
   constexpr int LB = ilog2(B);
   static_assert((1 << LB) == B, "batch bucket is a power of two");
   constexpr uint32_t STRIDE = OP == MKD_OP_QKV ? QKV_N / 2 : (OP == MKD_OP_GATEUP ? I / 2 : H / 2);
@@ -1666,15 +1676,19 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
   const uint32_t mine = f2bf(num / den);
   const uint32_t nbr = __shfl_xor(mine, 1, 64);
   {
-    // the pair (dd, dd + 1) as one word; its 8 replicas are stored by the four
-    // threads (dd even / odd, half 0 / 1) that hold it, two each
+    // the pair (dd, dd + 1) as one word; its p4_nrep replicas are stored by
+    // the four threads (dd even / odd, half 0 / 1) that hold it (PAIR: two
+    // threads, dd even / odd), spread evenly; a thread past the replica count
+    // stores none
     const uint64_t v = tw_make((dd & 1) ? (nbr | (mine << 16)) : (mine | (nbr << 16)), tag);
-    // (PAIR: two threads, dd even / odd, four each)
-    constexpr int NR = PAIR ? TW_NREP / 2 : TW_NREP / 4;
+    constexpr int HOLD = PAIR ? 2 : 4;
+    constexpr int NREP = p4_nrep<B>();
+    constexpr int NR = NREP / HOLD > 0 ? NREP / HOLD : 1;
     const size_t word = TW_ATTN + (size_t)b * (QS / 2) + ((size_t)(qh + hh) * HD + dd) / 2;
-    const int r0 = PAIR ? (dd & 1) * NR : ((dd & 1) * 2 + half) * NR;
+    const int r0 = (PAIR ? (dd & 1) : (dd & 1) * 2 + half) * NR;
 #pragma unroll
-    for (int r = 0; r < NR; r++) st_rep(c.ws, word, r0 + r, v);
+    for (int r = 0; r < NR; r++)
+      if (r0 + r < NREP) st_rep(c.ws, word, r0 + r, v);
   }
   return p4_agree(c, ok);  // also frees the scratch for the next task
 }
@@ -1997,7 +2011,7 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
               reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(__builtin_amdgcn_kernarg_segment_ptr())));
     return;
   }
-  P4 c{ws, p4_xcc_id() % TW_NREP, (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch), 0u}, flags,
+  P4 c{ws, p4_xcc_id() % p4_nrep<B>(), (uint32_t)flags[1], SyncLds{reinterpret_cast<uint32_t*>(scratch), 0u}, flags,
              reinterpret_cast<float*>(scratch + P4_SCR_RED), reinterpret_cast<float*>(scratch + P4_SCR_RES), xs,
              scratch + P4_SCR_ATTN, reinterpret_cast<uint32_t*>(scratch + P4_SCR_STAGE), 0, nullptr, 0,
              reinterpret_cast<float*>(scratch + p4_scr_part<B>())};

@@ -342,9 +342,12 @@ def test_pair_and_one_head_attention_long_ragged(batch, pair):
 def test_host_staged_rows_match_device_rows():
     """``decode_rows_host`` (pinned host staging, the engine's batch path) gives the
     same tokens and the same KV writes, bit for bit, as ``decode_rows`` on device
-    tensors, for 5 ragged rows (bucket 8) and then 1 row that rewrites the staging."""
+    tensors, for 5 ragged rows (bucket 8) and then 1 row that rewrites the staging.
+    (The host path sizes splits from the rows' positions, the device path from
+    the table width; the split count is pinned here so both run one schedule.)"""
     print("case: host-staged rows vs device rows, 5 rows then 1", flush=True)
     h = Harness(num_layers=2, num_blocks=16, kv_fill_seed=9, variant="tagged")
+    h.dec.splits_for = lambda *args, **kw: 2
     kv0 = h.kv.clone()
     cases = [([11, 22, 33, 44, 55], [700, 3, 256, 1023, 90], [[1, 2, 3], [4], [5, 6], [7, 8, 9, 10], [11]]),
              ([66], [300], [[12, 13]])]
