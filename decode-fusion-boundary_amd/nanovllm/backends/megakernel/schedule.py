@@ -94,19 +94,23 @@ def tagged_pair_heads(batch: int, max_context: int) -> bool:
     return int(batch) >= PAIR_HEADS_MIN_BATCH and int(max_context) >= PAIR_HEADS_MIN_CONTEXT
 
 
+B1_ONE_SPLIT_MAX = 192       # batch 1: one split up to this context,
+B1_EIGHT_SPLITS_MAX = 1700   # eight up to this one (one merge round of 7 partials), then 16
+
+
 def tagged_attn_splits(max_context: int, minimum: int = 1, batch: int = 1, pair_heads: bool = False) -> int:
     """Split-KV factor of the tagged persistent kernel: a power of two, at most
     16 // batch, never below ``minimum``.
 
-    Batch 1 aims at about 120 positions per split (log2 of max_context / 120
-    rounded to the nearest integer), batch 2 at 64 (rounded up), batch 4 and 8
-    at 256 (rounded up, as :func:`auto_attn_splits`). Measured on MI355X (device
-    us per step, tagged kernel, last split folding three partials per poll
-    round): batch 1 at ctx 100: 512 with 1 split, 538 with 2; ctx 480: 545 with
-    4, 579 with 8; ctx 1000: 597 with 8, 629 with 16; ctx 1800: 635 with 16, 661
-    with 8. Batch 2 at ctx 480: 616 with 8, 626 with 4; ctx 1000-1800: 8 best."""
-
-    import math
+    Batch 1: one split up to ctx 192, eight up to 1700 (the last split folds
+    the other seven's partials in one poll round of eight), then 16. Batch 2
+    aims at 64 positions per split (rounded up), batch 4 and 8 at 256 (rounded
+    up, as :func:`auto_attn_splits`). Measured on MI355X (device us per step,
+    tagged kernel, splits forced; 1 / 2 / 4 / 8 / 16): batch 1 at ctx 150: 537 /
+    555 / 544 / 545 / 574; ctx 300: 599 / 587 / 551 / 549 / 582; ctx 600: 744 /
+    650 / 583 / 562 / 595; ctx 1500: 1129 / 841 / 680 / 578 / 603; ctx 1900:
+    1288 / 924 / 736 / 630 / 611. Batch 2 at ctx 300-1500: 8 best (587 / 611 /
+    632 / 666 at ctx 300 / 600 / 1000 / 1500)."""
 
     b = max(1, int(batch))
     cap = max(1, MAX_SPLITS // b)
@@ -120,7 +124,7 @@ def tagged_attn_splits(max_context: int, minimum: int = 1, batch: int = 1, pair_
             splits *= 2
         return max(min(int(minimum), MAX_SPLITS), splits)
     if b == 1:
-        splits = 1 << max(0, round(math.log2(max(1.0, ctx / 120))))
+        splits = 1 if ctx <= B1_ONE_SPLIT_MAX else (8 if ctx <= B1_EIGHT_SPLITS_MAX else 16)
     elif b == 2:
         want = -(-ctx // 64)
         splits = 1

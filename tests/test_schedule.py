@@ -216,11 +216,12 @@ def test_stage_schedules_one_task_per_workgroup_with_published_residuals():
 
 
 def test_tagged_split_rule():
-    """The tagged kernel's measured split rule: ~120 positions per split at batch
-    1 (nearest power of two), 64 at batch 2, 256 at batch 4-8, capped at 16 // batch."""
+    """The tagged kernel's measured split rule: at batch 1 one split up to ctx 192,
+    eight up to 1700, then 16; 64 positions per split at batch 2, 256 at batch 4-8,
+    capped at 16 // batch."""
     from nanovllm.backends.megakernel.schedule import tagged_attn_splits as t
 
-    assert [t(c) for c in (1, 129, 161, 240, 480, 1000, 1864, 2048)] == [1, 1, 1, 2, 4, 8, 16, 16]
+    assert [t(c) for c in (1, 129, 192, 193, 480, 1000, 1700, 1701, 2048)] == [1, 1, 1, 8, 8, 8, 8, 16, 16]
     assert [t(c, batch=2) for c in (64, 65, 480, 1000, 2048)] == [1, 2, 8, 8, 8]
     assert [t(c, batch=8) for c in (200, 300, 2048)] == [1, 2, 2] and t(2048, batch=4) == 4
     assert t(100, minimum=4) == 4 and t(2048, minimum=16, batch=8) == 16
