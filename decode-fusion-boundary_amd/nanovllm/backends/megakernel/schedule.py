@@ -77,7 +77,6 @@ def batch_bucket(rows: int) -> int:
 
 PAIR_HEADS_MIN_BATCH = 4         # smallest batch bucket whose tagged kernel runs tasks of both query heads
 PAIR_HEADS_MIN_CONTEXT = 257     # and the shortest step context at which they are used
-PAIR_POSITIONS_PER_SPLIT = 256   # cached positions per split they aim at
 
 
 def tagged_pair_heads(batch: int, max_context: int) -> bool:
@@ -102,6 +101,12 @@ def tagged_attn_splits(max_context: int, minimum: int = 1, batch: int = 1, pair_
     """Split-KV factor of the tagged persistent kernel: a power of two, at most
     16 // batch, never below ``minimum``.
 
+    Tasks of both query heads (batch 4-8, two pages and more) take 32 // batch
+    splits: measured (1 / 2 / 4 / 8 splits) batch 4 at ctx 300: 772 / 764 / 727
+    / 720, ctx 1000: 1078 / 903 / 789 / 737; batch 8 (1 / 2 / 4 / 8) at ctx 300:
+    928 / 925 / 879 / 1035, ctx 450: 1019 / 965 / 894 / 1047, ctx 1000: 1236 /
+    1056 / 963 / 1122.
+
     Batch 1: one split up to ctx 192, eight up to 1700 (the last split folds
     the other seven's partials in one poll round of eight), then 16. Batch 2
     aims at 64 positions per split (rounded up), batch 4 and 8 at 256 (rounded
@@ -116,13 +121,10 @@ def tagged_attn_splits(max_context: int, minimum: int = 1, batch: int = 1, pair_
     cap = max(1, MAX_SPLITS // b)
     ctx = max(1, int(max_context))
     if pair_heads:
-        # half the tasks per split: up to 32 // batch splits (at most 16)
+        # half the tasks per split: 32 // batch splits (at most 16), the fastest
+        # at every context the both-head tasks run at (two pages and more)
         cap = max(1, min(MAX_SPLITS, 2 * MAX_SPLITS // b))
-        want = max(1, -(-ctx // PAIR_POSITIONS_PER_SPLIT))
-        splits = 1
-        while splits < want and splits < cap:
-            splits *= 2
-        return max(min(int(minimum), MAX_SPLITS), splits)
+        return max(min(int(minimum), MAX_SPLITS), cap)
     if b == 1:
         splits = 1 if ctx <= B1_ONE_SPLIT_MAX else (8 if ctx <= B1_EIGHT_SPLITS_MAX else 16)
     elif b == 2:

@@ -229,14 +229,14 @@ def test_tagged_split_rule():
 
 def test_pair_head_rule_and_its_split_rule():
     """Tasks of both query heads from batch 4 at contexts of two pages or more;
-    their split rule aims at 256 positions per split, capped at 32 // batch (16)."""
+    they take 32 // batch splits (at most 16)."""
     from nanovllm.backends.megakernel.schedule import tagged_attn_splits as t, tagged_pair_heads as p
 
     assert [p(b, 2000) for b in (1, 2, 4, 8)] == [False, False, True, True]
     assert [p(8, c) for c in (1, 256, 257, 2048)] == [False, False, True, True]
-    assert [t(c, batch=8, pair_heads=True) for c in (200, 300, 700, 1100, 2048)] == [1, 2, 4, 4, 4]
-    assert [t(c, batch=4, pair_heads=True) for c in (300, 1100, 2048)] == [2, 8, 8]
-    assert t(2048, batch=1, pair_heads=True) == 8 and t(10 ** 5, batch=1, pair_heads=True) == 16
+    assert [t(c, batch=8, pair_heads=True) for c in (300, 700, 1100, 2048)] == [4, 4, 4, 4]
+    assert [t(c, batch=4, pair_heads=True) for c in (300, 1100, 2048)] == [8, 8, 8]
+    assert t(2048, batch=1, pair_heads=True) == 16 and t(300, batch=2, pair_heads=True) == 16
     assert t(100, minimum=8, batch=8, pair_heads=True) == 8
     # a stage of pair tasks at the cap fills the 256 workgroups exactly once
     for b in (4, 8):
