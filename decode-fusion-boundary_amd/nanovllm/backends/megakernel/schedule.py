@@ -77,6 +77,8 @@ def batch_bucket(rows: int) -> int:
 
 PAIR_HEADS_MIN_BATCH = 4         # smallest batch bucket whose tagged kernel runs tasks of both query heads
 PAIR_HEADS_MIN_CONTEXT = 257     # and the shortest step context at which they are used
+PAIR_HEADS_MIN_CONTEXT_B8 = 193  # (batch 8: ctx 240 840 us with both heads, 4 splits; 861 one head, 2)
+ONE_HEAD_POSITIONS_PER_SPLIT = 192  # batch 4-8, one-head tasks (ctx 240 at batch 4: 701 us with 2, 730 with 1)
 
 
 def tagged_pair_heads(batch: int, max_context: int) -> bool:
@@ -90,7 +92,9 @@ def tagged_pair_heads(batch: int, max_context: int) -> bool:
     (ctx < 100) one-head tasks are faster (batch 8: 894 vs 911, batch 4: 694 vs
     706), and at batch 2, C5: 710 one-head vs 765 both heads."""
 
-    return int(batch) >= PAIR_HEADS_MIN_BATCH and int(max_context) >= PAIR_HEADS_MIN_CONTEXT
+    b = int(batch)
+    return b >= PAIR_HEADS_MIN_BATCH and int(max_context) >= (PAIR_HEADS_MIN_CONTEXT_B8 if b >= 8
+                                                               else PAIR_HEADS_MIN_CONTEXT)
 
 
 B1_ONE_SPLIT_MAX = 192       # batch 1: one split up to this context,
@@ -106,6 +110,9 @@ def tagged_attn_splits(max_context: int, minimum: int = 1, batch: int = 1, pair_
     / 720, ctx 1000: 1078 / 903 / 789 / 737; batch 8 (1 / 2 / 4 / 8) at ctx 300:
     928 / 925 / 879 / 1035, ctx 450: 1019 / 965 / 894 / 1047, ctx 1000: 1236 /
     1056 / 963 / 1122.
+
+    One-head tasks at batch 4-8 aim at 192 positions per split (rounded up to
+    a power of two, capped at 16 // batch).
 
     Batch 1: one split up to ctx 192, eight up to 1700 (the last split folds
     the other seven's partials in one poll round of eight), then 16. Batch 2
@@ -133,7 +140,10 @@ def tagged_attn_splits(max_context: int, minimum: int = 1, batch: int = 1, pair_
         while splits < want:
             splits *= 2
     else:
-        return auto_attn_splits(ctx, minimum, b)
+        want = -(-ctx // ONE_HEAD_POSITIONS_PER_SPLIT)
+        splits = 1
+        while splits < want:
+            splits *= 2
     return max(min(int(minimum), MAX_SPLITS), min(splits, cap))
 
 

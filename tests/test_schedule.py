@@ -223,17 +223,20 @@ def test_tagged_split_rule():
 
     assert [t(c) for c in (1, 129, 192, 193, 480, 1000, 1700, 1701, 2048)] == [1, 1, 1, 8, 8, 8, 8, 16, 16]
     assert [t(c, batch=2) for c in (64, 65, 480, 1000, 2048)] == [1, 2, 8, 8, 8]
-    assert [t(c, batch=8) for c in (200, 300, 2048)] == [1, 2, 2] and t(2048, batch=4) == 4
+    # one-head tasks at batch 4-8: 192 positions per split, capped at 16 // batch
+    assert [t(c, batch=8) for c in (192, 193, 2048)] == [1, 2, 2] and t(2048, batch=4) == 4
+    assert [t(c, batch=4) for c in (192, 193, 400)] == [1, 2, 4]
     assert t(100, minimum=4) == 4 and t(2048, minimum=16, batch=8) == 16
 
 
 def test_pair_head_rule_and_its_split_rule():
-    """Tasks of both query heads from batch 4 at contexts of two pages or more;
-    they take 32 // batch splits (at most 16)."""
+    """Tasks of both query heads from batch 4 at contexts of two pages or more
+    (batch 8: from ctx 193); they take 32 // batch splits (at most 16)."""
     from nanovllm.backends.megakernel.schedule import tagged_attn_splits as t, tagged_pair_heads as p
 
     assert [p(b, 2000) for b in (1, 2, 4, 8)] == [False, False, True, True]
-    assert [p(8, c) for c in (1, 256, 257, 2048)] == [False, False, True, True]
+    assert [p(8, c) for c in (1, 192, 193, 2048)] == [False, False, True, True]
+    assert [p(4, c) for c in (1, 256, 257, 2048)] == [False, False, True, True]
     assert [t(c, batch=8, pair_heads=True) for c in (300, 700, 1100, 2048)] == [4, 4, 4, 4]
     assert [t(c, batch=4, pair_heads=True) for c in (300, 1100, 2048)] == [8, 8, 8]
     assert t(2048, batch=1, pair_heads=True) == 16 and t(300, batch=2, pair_heads=True) == 16
