@@ -1761,6 +1761,14 @@ __device__ __forceinline__ void dma_decode_attn(DmaTask& t, const uint8_t* karg,
   t.lds0 = g.c_end;
 }
 
+// Cache policy of the ring copies (weights and KV cache): non-temporal (the
+// gfx950 nt bit). Every byte is read once per step, and with the default policy
+// each hand-over's burst of streamed lines competes with the tagged words that
+// the whole grid polls at that moment for the memory-side cache. Measured: batch
+// 1/2/4/8 -17/-14/-14/-13 us, C5 batch 8 -25 us, C4 batch 8 -14 us. (sc0 or
+// sc1 alone: no change.)
+constexpr int DMA_NT = 2;
+
 // KV chunk j of ATTN task t into `slot` (this DMA wave's 4 units). A cached
 // position's block id outside [0, num_blocks) is reported as ERR_BAD_INPUT and
 // clamped, so no copy leaves the cache.
@@ -1782,7 +1790,7 @@ __device__ __forceinline__ void dma_issue_attn(const DmaTask& t, int j, uint8_t*
     const int q = k < 2 ? ((s16 - (p & 1)) & 15) : s16;  // source piece (K: unswizzled)
     const int pr = P0 + p < t.lds0 ? p : 0;
     const uint16_t* src = (k < 2 ? t.b0 : t.b1) + (row0 + pr) * KVS + q * 8;
-    __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(slot + u * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(slot + u * 1024), 16, 0, DMA_NT);
   }
 }
 
@@ -1868,7 +1876,7 @@ __device__ __forceinline__ void dma_issue(DmaTask& t, int j, uint8_t* slot, int 
       const int r = K == 1024 ? 2 * k + (dw >> 1) : (K == 2048 ? k : dw >> 1);
       const int src_lane = (lane + r) & 63;
       __builtin_amdgcn_global_load_lds((gbl_void_t*)(t.src + k * t.kstep + src_lane * 8),
-                                       (lds_void_t*)(slot + t.lds0 + k * t.ldsk), 16, 0, 0);
+                                       (lds_void_t*)(slot + t.lds0 + k * t.ldsk), 16, 0, DMA_NT);
     }
     t.src += t.cstep;
     return;
@@ -1882,7 +1890,7 @@ __device__ __forceinline__ void dma_issue(DmaTask& t, int j, uint8_t* slot, int 
                                           : t.b0 + (size_t)r * t.stride;
     const int src_lane = (lane + (u - u0) / PR) & 63;
     __builtin_amdgcn_global_load_lds((gbl_void_t*)(row + p * 512 + src_lane * 8), (lds_void_t*)(slot + (u - u0) * 1024),
-                                     16, 0, 0);
+                                     16, 0, DMA_NT);
   }
 }
 
