@@ -275,8 +275,12 @@ constexpr int largest_divisor_le8(int n) {
 template <int B, int K>
 __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t tag) {
   constexpr int PER = B * (K / 2) / 256;  // words per thread
-  // (batch 8, down: 12-word groups, four rounds instead of six)
-  constexpr int NB = B >= 8 && K == 3072 ? 12 : largest_divisor_le8(PER);
+  // Words polled as one group (one round in flight per group). Batch 8 polls
+  // the most words per hand-over: down input 48 words per thread in two groups
+  // of 24, o_proj input 32 in two of 16 (measured against 12 / 8: batch 8
+  // -21 us, C4 -24 us; one group of 48 or 32: +150 / +65 us, register bound).
+  // Larger groups at batch 2 and 4 measured no faster.
+  constexpr int NB = B >= 8 && K == 3072 ? 24 : (B >= 8 && K == 2048 ? 16 : largest_divisor_le8(PER));
   static_assert(PER % NB == 0, "whole groups");
   const int t = p4_tid();
   const uint64_t* src = c.ws.tw(base + (size_t)c.rep * TW_GROUP);
@@ -351,7 +355,7 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
     }
   } else if (rk.valid) {
     // hidden words only: rows in groups of GH (2 words each)
-    constexpr int GH = B < 4 ? B : 4;
+    constexpr int GH = B < 4 ? B : 4;  // (8 at batch 8: +58 us, measured)
     auto haddr = [&](int b0) {
       return [=](int k) { return c.ws.tw(hid + (size_t)c.rep * TW_GROUP + (size_t)(b0 + (k >> 1)) * (H / 2) + 2 * t + (k & 1)); };
     };
@@ -882,8 +886,6 @@ __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int ro
       atomicMax(reinterpret_cast<unsigned long long*>(tr + 6), (unsigned long long)wall_clock64());
 #endif
     if ((cc + j) % P4G<NS>::G == 0) raw_barrier();  // group of G chunks handed over
-
-
 #ifdef MKD_TRACE_CHUNKS
     // debug: chunk release and compute-end times after the task trace ([grid][512][2])
     uint64_t* ct = dbg_chunks == nullptr ? nullptr : dbg_chunks + ((size_t)blockIdx.x * 512 + ((cc + j) & 511)) * 2;
