@@ -355,7 +355,7 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
     }
   } else if (rk.valid) {
     // hidden words only: rows in groups of GH (2 words each)
-    constexpr int GH = B < 4 ? B : 4;  // (8 at batch 8: +58 us, measured)
+    constexpr int GH = B < 4 ? B : 4;  // (8 at batch 8: +54 us, measured)
     auto haddr = [&](int b0) {
       return [=](int k) { return c.ws.tw(hid + (size_t)c.rep * TW_GROUP + (size_t)(b0 + (k >> 1)) * (H / 2) + 2 * t + (k & 1)); };
     };
@@ -437,15 +437,21 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
   for (int b = 0; b < B; b++) {
     float ss = s[b][0] * s[b][0] + s[b][1] * s[b][1] + s[b][2] * s[b][2] + s[b][3] * s[b][3];
     ss = wave_sum(ss);
-    if (lane == 0) c.red[wave * MAXB + b] = ss;
+    if (lane == 0) c.red[b * PK_CW + wave] = ss;  // [row][wave]
   }
   p4_trace_at(c, 4);
   if (!p4_agree(c, ok)) return false;
   p4_trace_at(c, 5);
+  // lane b < B reads row b's four wave sums with one 16-byte LDS read and
+  // computes its scale; the rows' scales are then read back lane by lane (a
+  // uniform read per row of each wave sum made the compiler chain 4 B LDS
+  // round trips, 1.3 us at batch 8)
+  const float4 wsum = *reinterpret_cast<const float4*>(c.red + PK_CW * (lane & (B - 1)));
+  const float r_lane =
+      __builtin_amdgcn_rsqf((((wsum.x + wsum.y) + wsum.z) + wsum.w) * (1.0f / H) + EPS);  // v_rsq_f32 (1 ulp)
 #pragma unroll
   for (int b = 0; b < B; b++) {
-    const float tot = c.red[b] + c.red[MAXB + b] + c.red[2 * MAXB + b] + c.red[3 * MAXB + b];
-    const float r = __builtin_amdgcn_rsqf(tot * (1.0f / H) + EPS);  // v_rsq_f32 (1 ulp)
+    const float r = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r_lane), b));
     // bf16(bf16(s * r) * w), pairwise through the packed conversion
     const uint32_t n01 = pack_bf2(s[b][0] * r, s[b][1] * r), n23 = pack_bf2(s[b][2] * r, s[b][3] * r);
     *reinterpret_cast<uint2*>(c.xs + (size_t)b * XS_H + k0) =
