@@ -2040,7 +2040,15 @@ __global__ __launch_bounds__(PK_THREADS, 1) void k_persistent4(MkdStepDesc d, Mk
   for (int i = 0; i < n_inst; i++) {
     const Inst w = w_next;
     if (i + 1 < n_inst) w_next = load_inst(crow + (i + 1) * MKD_INST_WORDS);  // in flight during this task
-    uint64_t* tr = d.trace != nullptr ? d.trace + ((size_t)blockIdx.x * s.max_inst + i) * P4_TR_STRIDE : nullptr;
+    // per-task time stamps (MkdStepDesc::trace, a debugging aid): compiled into
+    // builds with MKD_TRACE_TASKS and into the batch-8 kernel; the other
+    // kernels leave them out (batch 1/2/4 -3/-6/-4 us; left out at batch 8 the
+    // smaller kernel measured 19 us slower)
+    uint64_t* tr = nullptr;
+#ifndef MKD_TRACE_TASKS
+    if constexpr (B >= 8)
+#endif
+      tr = d.trace != nullptr ? d.trace + ((size_t)blockIdx.x * s.max_inst + i) * P4_TR_STRIDE : nullptr;
     if (tr != nullptr && threadIdx.x == 0) tr[0] = wall_clock64();
     c.trp = tr;
     c.task = i;

@@ -124,7 +124,8 @@ typedef struct MkdStepDesc {
   int32_t _pad1;
   /* optional [grid][max_inst][4] uint64 timestamps (100 MHz device clock) of
    * the persistent kernel's tasks: start, dependency met, inputs staged, done;
-   * NULL to skip (diagnostics only) */
+   * NULL to skip (diagnostics only: written by the batch-8 kernel, and by every
+   * batch's kernel in a library built with -DMKD_TRACE_TASKS) */
   uint64_t* trace;
 } MkdStepDesc;
 
