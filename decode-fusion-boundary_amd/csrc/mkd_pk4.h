@@ -1016,12 +1016,13 @@ constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
 // Replicas of the all-read tagged words this batch's kernel writes (the
 // workspace holds TW_NREP); workgroups on XCD x read replica x % p4_nrep.
 // Measured per batch (us per step with 8 / 4 / 2 / 1 replicas): batch 1 479 /
-// 481 / 492 / 516; batch 4 610 / 603 / 602 / 614; batch 8 758 / 727 / 723 /
-// 723 (C4 867 / 833 / 831 / 828): at batch 4-8 the replica stores cost more
-// than spreading the reads over more copies saves.
+// 481 / 492 / 516; batch 2 528 / 525 / 530 (C5 647 / 644 / 650); batch 4 610 /
+// 603 / 602 / 614; batch 8 758 / 727 / 723 / 723 (C4 867 / 833 / 831 / 828):
+// from batch 2 on the replica stores cost more than spreading the reads over
+// more copies saves.
 template <int B>
 constexpr int p4_nrep() {
-  return B >= 8 ? 1 : (B >= 4 ? 2 : TW_NREP);
+  return B >= 8 ? 1 : (B >= 4 ? 2 : (B == 2 ? 4 : TW_NREP));
 }
 
 // The residual words this task's owner threads staged in its prologue: one
