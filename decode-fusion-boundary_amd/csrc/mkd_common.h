@@ -162,6 +162,65 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_mov<0x143, 0xC>(v, 0.f);   // row_bcast31 -> rows 2, 3
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// Wave totals of B (2, 4 or 8) per-lane values at once: lane l returns the
+// total of value l % B. A reduce-scatter over lane bits 0 .. log2 B - 1 (each
+// step keeps half of the values and adds the partner's other half: quad swaps,
+// then row_shl / row_shr by 4), then an all-reduce over the remaining bits
+// (row_ror 8, the gfx950 permlane16 / permlane32 swaps): 11 cross-lane moves
+// at B = 8 where B separate wave_sum chains take 6 B and B lane reads.
+template <int B>
+__device__ __forceinline__ float rows_wave_sum(const float (&x)[B]) {
+  static_assert(B == 2 || B == 4 || B == 8, "2, 4 or 8 values");
+  const int l = threadIdx.x & 63;
+  float v[B];
+#pragma unroll
+  for (int j = 0; j < B; j++) v[j] = x[j];
+  {  // lane bit 0: keep values of index bit 0 = the lane's bit 0
+    const bool p = l & 1;
+#pragma unroll
+    for (int j = 0; j < B / 2; j++) {
+      const float keep = p ? v[2 * j + 1] : v[2 * j], send = p ? v[2 * j] : v[2 * j + 1];
+      v[j] = keep + dpp_mov<0xB1>(send, 0.f);  // quad_perm [1,0,3,2]
+    }
+  }
+  if constexpr (B >= 4) {  // lane bit 1
+    const bool p = l & 2;
+#pragma unroll
+    for (int j = 0; j < B / 4; j++) {
+      const float keep = p ? v[2 * j + 1] : v[2 * j], send = p ? v[2 * j] : v[2 * j + 1];
+      v[j] = keep + dpp_mov<0x4E>(send, 0.f);  // quad_perm [2,3,0,1]
+    }
+  }
+  // lane bit 2: the partner l ^ 4 is l + 4 (row_shl 4) or l - 4 (row_shr 4).
+  // Both moves run with every lane active (a DPP move reads 0 from a lane
+  // that is off): the empty asm keeps the compiler from moving each into its
+  // side of a branch on the lane's bit.
+  const bool p2 = l & 4;
+  auto xor4 = [&](float send) {
+    float up = dpp_mov<0x104>(send, 0.f), down = dpp_mov<0x114>(send, 0.f);
+    asm volatile("" : "+v"(up), "+v"(down));
+    return p2 ? down : up;
+  };
+  float w;
+  if constexpr (B >= 8) {
+    const float keep = p2 ? v[1] : v[0], send = p2 ? v[0] : v[1];
+    w = keep + xor4(send);
+  } else {
+    w = v[0];
+    if constexpr (B == 2) w += dpp_mov<0x4E>(w, 0.f);  // lane bit 1
+    w += xor4(w);
+  }
+  w += dpp_mov<0x128>(w, 0.f);  // lane bit 3: row_ror 8
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w), __float_as_uint(w), false, false);
+    w = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // lane bit 4
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(w), __float_as_uint(w), false, false);
+    w = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // lane bit 5
+  }
+  return w;
+}
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_mov<0xB1>(v, -INFINITY));
   v = fmaxf(v, dpp_mov<0x4E>(v, -INFINITY));

@@ -433,11 +433,16 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
       stage[((t - res_first) * B + b) * 2 + 1] = rk.w[b][1];
     }
   }
+  if constexpr (B == 1) {
+    const float ss = wave_sum(s[0][0] * s[0][0] + s[0][1] * s[0][1] + s[0][2] * s[0][2] + s[0][3] * s[0][3]);
+    if (lane == 0) c.red[wave] = ss;  // [row][wave]
+  } else {
+    // all rows' sums of squares in one reduction (lane b ends with row b's)
+    float sq[B];
 #pragma unroll
-  for (int b = 0; b < B; b++) {
-    float ss = s[b][0] * s[b][0] + s[b][1] * s[b][1] + s[b][2] * s[b][2] + s[b][3] * s[b][3];
-    ss = wave_sum(ss);
-    if (lane == 0) c.red[b * PK_CW + wave] = ss;  // [row][wave]
+    for (int b = 0; b < B; b++) sq[b] = s[b][0] * s[b][0] + s[b][1] * s[b][1] + s[b][2] * s[b][2] + s[b][3] * s[b][3];
+    const float ss = rows_wave_sum<B>(sq);
+    if (lane < B) c.red[lane * PK_CW + wave] = ss;  // [row][wave]
   }
   p4_trace_at(c, 4);
   if (!p4_agree(c, ok)) return false;
