@@ -612,31 +612,49 @@ __device__ __forceinline__ void chunk_mfma4(const uint8_t* slot, const uint4* x4
                                                            acc[g][h], 0, 0, 0);
       }
   }
-  // sum over the 16 blocks: lanes i, i + 4, ..., i + 60 (rotations by 4 and 8
-  // within each row of 16 lanes, then across the rows)
+  // sum over the 16 blocks (lane bits 2-5) of the NV = 4 NH values of each
+  // lane, as a transpose-reduce: lane bits 2 .. 1 + log2 NV each halve the
+  // values a lane keeps (it adds its partner's half), the remaining bits are
+  // summed whole; lane l then holds value j = (l >> 2) % NV, batch row j, of
+  // weight row l % 4 (12 cross-lane moves at batch 8 instead of 32)
+  static_assert(NG == 1, "chunk_mfma4 serves K >= 2048: at most 4 rows per chunk");
+  constexpr int NV = 4 * NH;
+  float v[NV];
 #pragma unroll
-  for (int g = 0; g < NG; g++)
+  for (int h = 0; h < NH; h++)
 #pragma unroll
-    for (int h = 0; h < NH; h++)
+    for (int m = 0; m < 4; m++) v[4 * h + m] = acc[0][h][m];
+  {  // lane bit 2: partner lane ^ 4 is lane + 4 (row_shl 4) or lane - 4 (row_shr 4); both
+     // moves run with every lane active (the empty asm keeps each out of a branch)
+    const bool p = lane & 4;
 #pragma unroll
-      for (int m = 0; m < 4; m++) {
-        float v = acc[g][h][m];
-        v += dpp_mov<0x124>(v, 0.f);  // row_ror:4
-        v += dpp_mov<0x128>(v, 0.f);  // row_ror:8
-        acc[g][h][m] = xor32_sum(xor16_sum(v));
-      }
-  if (lane < 4) {
-#pragma unroll
-    for (int g = 0; g < NG; g++) {
-      const int row = 4 * g + lane;
-      if (row < RPC) {
-#pragma unroll
-        for (int h = 0; h < NH; h++)
-          *reinterpret_cast<float4*>(part + (size_t)(wave * 32 + row) * B + 4 * h) =
-              make_float4(acc[g][h][0], acc[g][h][1], acc[g][h][2], acc[g][h][3]);
-      }
+    for (int j = 0; j < NV / 2; j++) {
+      const float keep = p ? v[2 * j + 1] : v[2 * j], send = p ? v[2 * j] : v[2 * j + 1];
+      float up = dpp_mov<0x104>(send, 0.f), down = dpp_mov<0x114>(send, 0.f);
+      asm volatile("" : "+v"(up), "+v"(down));
+      v[j] = keep + (p ? down : up);
     }
   }
+  {  // lane bit 3: row_ror 8
+    const bool p = lane & 8;
+#pragma unroll
+    for (int j = 0; j < NV / 4; j++) {
+      const float keep = p ? v[2 * j + 1] : v[2 * j], send = p ? v[2 * j] : v[2 * j + 1];
+      v[j] = keep + dpp_mov<0x128>(send, 0.f);
+    }
+  }
+  float t = v[0];
+  if constexpr (NV == 8) {  // lane bit 4 halves once more: the partner's value through the permlane16 swap
+    const bool p = lane & 16;
+    const float keep = p ? v[1] : v[0], send = p ? v[0] : v[1];
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(send), __float_as_uint(send), false, false);
+    t = keep + __uint_as_float(p ? r[0] : r[1]);
+  } else {
+    t = xor16_sum(t);
+  }
+  t = xor32_sum(t);
+  const int row = lane & 3, j = (lane >> 2) & (NV - 1);
+  if (row < RPC && lane < 4 * NV) part[(size_t)(wave * 32 + row) * B + j] = t;
 }
 // GEMV chunks on chunk_mfma4: K = 2048 and 3072 (o_proj, down: 4 and 2 rows
 // per chunk) at batch 4 and 8. Measured per chunk at batch 8: down 1.06 ->
@@ -1688,7 +1706,9 @@ __device__ __forceinline__ bool p4_attn(const MkdStepDesc& d, const P4& c, int l
     }
   }
   const uint32_t mine = f2bf(num / den);
-  const uint32_t nbr = __shfl_xor(mine, 1, 64);
+  // the neighbouring dimension's value: a DPP quad swap (every lane active
+  // here), not an LDS-crossbar round trip
+  const uint32_t nbr = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mine, 0xB1, 0xF, 0xF, false);
   {
     // the pair (dd, dd + 1) as one word; its p4_nrep replicas are stored by
     // the four threads (dd even / odd, half 0 / 1) that hold it (PAIR: two
