@@ -65,8 +65,20 @@ constexpr int XS_H = H + 8;
 // Activation rows of K = 2048 and 3072 are not padded (the batch-4 ring would
 // lose a slot): 16-byte piece q of row b is stored at piece q ^ (b mod 8).
 __device__ __forceinline__ int xs_piece(int b, int q) { return q ^ (b & 7); }
-// float [4 waves][32 rows][B] partial sums of the MFMA GEMV (batch >= MFMA_MIN_B),
+// float partial sums of the MFMA GEMV (batch >= MFMA_MIN_B): [32 rows][B][4 waves]
+// at batch 2 (a result's four wave partials are one 16-byte read for the store
+// epilogue: batch 2 -3 us, C5 batch 2 -7), [4 waves][32 rows][B] at batch 4-8
+// (where the MFMA tile writes 4 batch rows with one 16-byte store: the other
+// layout measured +1 us at batch 4, +2 to +3 us at batch 8),
 // after the attention scratch (batch 2, 4: 1, 2 KiB) or in the 4 KiB added at batch 8
+template <int B>
+constexpr bool p4_part_rows_first() { return B == 2; }
+// index of entry (row, b, wave) of the partial tile (row < 32, b < B, wave < 4)
+template <int B>
+__device__ __forceinline__ size_t p4_part_at(int row, int b, int wave) {
+  if constexpr (p4_part_rows_first<B>()) return ((size_t)row * B + b) * PK_CW + wave;
+  else return ((size_t)wave * 32 + row) * B + b;
+}
 template <int B>
 constexpr int p4_scr_part() { return B >= 8 ? PK_SCRATCH : 5632; }
 static_assert(5632 + 4 * 32 * 4 * 4 <= PK_SCRATCH && P4_SCR_ATTN + 3104 <= 5632, "partial tile overlaps");
@@ -509,8 +521,8 @@ typedef float p4_f32x4 __attribute__((ext_vector_type(4)));
 // beyond B and RPC repeat real ones and their results are dropped), in two
 // accumulator chains. Lane l supplies row / column l % 16 and K elements
 // 8 (l / 16) .. + 7 of each 32-wide step; result lane l holds column l % 16,
-// rows 4 (l / 16) .. + 3. The wave's partial sums go to
-// part[(w * 32 + row) * B + b] (part offset by the chunk's first row); the
+// rows 4 (l / 16) .. + 3. The wave's partial sums go to entry (row, b, w) of
+// the partial tile (p4_part_at; part offset by the chunk's first row); the
 // store epilogue adds the four waves' partials in a fixed order.
 template <int B, int K>
 __device__ __forceinline__ void chunk_mfma(const uint8_t* slot, const uint4* x4, float* part) {
@@ -541,13 +553,21 @@ __device__ __forceinline__ void chunk_mfma(const uint8_t* slot, const uint4* x4,
     }
   }
   const p4_f32x4 acc = a0 + a1;
-  if constexpr (B >= 4) {
+  if constexpr (!p4_part_rows_first<B>()) {
     if (n < RPC && 4 * kg < B)
-      *reinterpret_cast<float4*>(part + (size_t)(wave * 32 + n) * B + 4 * kg) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      *reinterpret_cast<float4*>(part + p4_part_at<B>(n, 4 * kg, wave)) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  } else if constexpr (B >= 4) {
+    if (n < RPC && 4 * kg < B) {
+#pragma unroll
+      for (int m = 0; m < 4; m++) part[p4_part_at<B>(n, 4 * kg + m, wave)] = acc[m];
+    }
   } else if constexpr (B == 2) {
-    if (n < RPC && kg == 0) *reinterpret_cast<float2*>(part + (size_t)(wave * 32 + n) * B) = make_float2(acc[0], acc[1]);
+    if (n < RPC && kg == 0) {
+      part[p4_part_at<B>(n, 0, wave)] = acc[0];
+      part[p4_part_at<B>(n, 1, wave)] = acc[1];
+    }
   } else {
-    if (n < RPC && kg == 0) part[(size_t)(wave * 32 + n) * B] = acc[0];
+    if (n < RPC && kg == 0) part[p4_part_at<B>(n, 0, wave)] = acc[0];
   }
 }
 // x[lane] + x[lane ^ 32] and x[lane] + x[lane ^ 16] on every lane (gfx950
@@ -568,8 +588,8 @@ __device__ __forceinline__ float xor16_sum(float x) {
 // reads the chunk's few weight rows and the batch rows many times over:
 // measured LDS-bound at batch 8). Wave w takes K quarter w in 128-element steps
 // (lane 4 blk + i: piece blk of the step, batch row 4 h + i of x, weight row
-// 4 g + i), the 16 blocks' sums are added across lanes, and lanes 0-3 write
-// part[(w * 32 + row) * B + b] as chunk_mfma does. Rows past the chunk's
+// 4 g + i), the 16 blocks' sums are added across lanes and written to
+// entry (row, b, w) of the partial tile as chunk_mfma does. Rows past the chunk's
 // (K = 3072: 2 of a group's 4) repeat its rows and are not written.
 template <int B, int K>
 __device__ __forceinline__ void chunk_mfma4(const uint8_t* slot, const uint4* x4, float* part) {
@@ -654,7 +674,7 @@ __device__ __forceinline__ void chunk_mfma4(const uint8_t* slot, const uint4* x4
   }
   t = xor32_sum(t);
   const int row = lane & 3, j = (lane >> 2) & (NV - 1);
-  if (row < RPC && lane < 4 * NV) part[(size_t)(wave * 32 + row) * B + j] = t;
+  if (row < RPC && lane < 4 * NV) part[p4_part_at<B>(row, j, wave)] = t;
 }
 // GEMV chunks on chunk_mfma4: K = 2048 and 3072 (o_proj, down: 4 and 2 rows
 // per chunk) at batch 4 and 8. Measured per chunk at batch 8: down 1.06 ->
@@ -922,8 +942,8 @@ __device__ __forceinline__ void p4_chunks(uint8_t* ring, int cc, int nch, int ro
 #endif
     if constexpr (std::is_same<Out, PartSink>::value) {
       if (!aborted) {
-        if constexpr (p4_mfma4<B, K>()) chunk_mfma4<B, K>(slot, xsrc.x4, out.part + (size_t)j * RPC * B);
-        else chunk_mfma<B, K>(slot, xsrc.x4, out.part + (size_t)j * RPC * B);
+        if constexpr (p4_mfma4<B, K>()) chunk_mfma4<B, K>(slot, xsrc.x4, out.part + p4_part_at<B>(j * RPC, 0, 0));
+        else chunk_mfma<B, K>(slot, xsrc.x4, out.part + p4_part_at<B>(j * RPC, 0, 0));
       }
     } else if constexpr (std::is_same<Out, LmSink>::value) {
       // (every wave still takes each hand-over barrier above)
@@ -1104,8 +1124,13 @@ __device__ __forceinline__ void p4_store_op(const P4& c, const Inst& w) {
     // GEMV) the four waves' partial sums, added in a fixed order
     auto R = [&](int row) -> float {
       if constexpr (p4_mfma_op<B, OP>()) {
-        const float* p = c.part + (size_t)row * B + b;
-        return (p[0] + p[32 * B]) + (p[64 * B] + p[96 * B]);
+        if constexpr (p4_part_rows_first<B>()) {
+          const float4 q = *reinterpret_cast<const float4*>(c.part + p4_part_at<B>(row, b, 0));
+          return (q.x + q.y) + (q.z + q.w);  // waves 0-3, one 16-byte read
+        } else {
+          const float* p = c.part + p4_part_at<B>(row, b, 0);
+          return (p[0] + p[32 * B]) + (p[64 * B] + p[96 * B]);
+        }
       } else {
         return c.res[row * MAXB + b];
       }
