@@ -51,6 +51,7 @@ CONFIGS = {
     "c4_b8": ([(4099 * (b + 1)) % V for b in range(8)], [512 + 16 * b for b in range(8)], None, 26),
     "c5_b1": ([31337], [1900], None, 9),
     "c5_b2": ([12, 150000], [1700, 1100], None, 13),
+    "c5_b4": ([7, 90001, 123456, 4242], [1500, 1200, 1900, 1100], None, 26),
 }
 
 
