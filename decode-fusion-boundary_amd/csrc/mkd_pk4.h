@@ -204,15 +204,43 @@ __device__ __forceinline__ void p4_trace_poll(const P4& c) {
 // First round of a poll: issue the loads (returned in a[]). Issuing it before
 // a task's other loads matters: loads complete in issue order, so a check of
 // a[] then waits only for loads issued before it.
+// Two adjacent tagged words (16-byte aligned) with one 16-byte buffer load at
+// device scope (sc1, as ld_co); each word keeps its own tag, so a pair seen
+// half written is polled again.
+struct PairAddr {
+  __amdgpu_buffer_rsrc_t r;
+  uint32_t off;  // bytes
+};
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pair_rsrc(const uint64_t* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(base), 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ void ld_co2(PairAddr pa, uint64_t& lo, uint64_t& hi) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(pa.r, pa.off, 0, 16 /* sc1 */);
+  lo = (uint64_t)q.x | ((uint64_t)q.y << 32);
+  hi = (uint64_t)q.z | ((uint64_t)q.w << 32);
+}
+// One round of N word loads; PAIRS: words 2j and 2j + 1 are adjacent and come
+// from one 16-byte load.
+template <int N, bool PAIRS, class Addr>
+__device__ __forceinline__ void poll_round(Addr addr, uint64_t (&a)[N]) {
+  if constexpr (PAIRS) {
+    static_assert(N % 2 == 0, "whole pairs");
+#pragma unroll
+    for (int k = 0; k < N; k += 2) ld_co2(addr(k), a[k], a[k + 1]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < N; k++) a[k] = ld_co(addr(k));
+  }
+}
 template <int N, class Addr>
 __device__ __forceinline__ void poll_issue(Addr addr, uint64_t (&a)[N]) {
-#pragma unroll
-  for (int k = 0; k < N; k++) a[k] = ld_co(addr(k));
+  poll_round<N, false>(addr, a);
 }
 // Check the first round and keep polling until every word carries `tag`
 // (one round in flight: measured no slower than two, with half the traffic;
 // re-polling only one word while the others are missing measured slower).
-template <int N, class Addr>
+template <int N, bool PAIRS = false, class Addr>
 __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_t (&v)[N], uint32_t tag,
                                             const Ws& ws) {
   // The device error word and the clock are read only by a poll that has
@@ -250,18 +278,17 @@ __device__ __forceinline__ bool poll_finish(Addr addr, uint64_t (&a)[N], uint64_
     }
     __builtin_amdgcn_s_sleep(0);  // (longer pauses measured slower at every batch size; 0 vs 1: -1 to -3 us)
     if ((spin & 63u) == 62u) err = ld_co(ws.line(CTR_ERR));
-#pragma unroll
-    for (int k = 0; k < N; k++) a[k] = ld_co(addr(k));
+    poll_round<N, PAIRS>(addr, a);
   }
 }
 // Load N tagged words (addr(k), k < N) and spin until each carries `tag`.
 // Returns false on a timeout (which it reports) or when another workgroup
 // has reported an error.
-template <int N, class Addr>
+template <int N, bool PAIRS = false, class Addr>
 __device__ __forceinline__ bool poll_tagged(Addr addr, uint64_t (&v)[N], uint32_t tag, const Ws& ws) {
   uint64_t a[N];
-  poll_issue<N>(addr, a);
-  return poll_finish<N>(addr, a, v, tag, ws);
+  poll_round<N, PAIRS>(addr, a);
+  return poll_finish<N, PAIRS>(addr, a, v, tag, ws);
 }
 
 // Compute-wave barrier that also agrees on an abort over the four waves.
@@ -298,18 +325,40 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
   const uint64_t* src = c.ws.tw(base + (size_t)c.rep * TW_GROUP);
   uint32_t* dst = reinterpret_cast<uint32_t*>(c.xs);
   bool ok = true;
+  if constexpr (B >= 2) {
+    // words polled in pairs: word slot w of this thread is element w % 2 of pair
+    // t + 256 (w / 2) of [B][K/2], one 16-byte load per pair (half the load
+    // instructions of a round: batch 8 -30 us, C4 -28, C5 batch 8 -34, batch 4
+    // -9; batch 1, with 4-6 words per thread, measured +4 us and keeps words)
+    constexpr int WPR2 = K / 1024;  // 256-pair blocks per row
 #pragma unroll
-  for (int k0 = 0; k0 < PER; k0 += NB) {
-    uint64_t v[NB];
-    ok = ok && poll_tagged<NB>([&](int k) { return src + t + 256 * (k0 + k); }, v, tag, c.ws);
-    if (k0 == 0) p4_trace_poll(c);
+    for (int k0 = 0; k0 < PER; k0 += NB) {
+      uint64_t v[NB];
+      const __amdgpu_buffer_rsrc_t rs = pair_rsrc(src);
+      ok = ok && poll_tagged<NB, true>(
+                     [&](int k) { const int w = k0 + k; return PairAddr{rs, (uint32_t)(16 * (t + 256 * (w >> 1)))}; },
+                     v, tag, c.ws);
+      if (k0 == 0) p4_trace_poll(c);
 #pragma unroll
-    for (int k = 0; k < NB; k++) {
-      // word t + 256 m of [B][K/2]: row m / WPR, word 256 (m % WPR) + t of it,
-      // its 16-byte piece XOR-swizzled by the row (xs_piece)
-      constexpr int WPR = K / 2 / 256;
-      const int m = k0 + k, b = m / WPR, ww = 256 * (m % WPR) + t;
-      dst[b * (K / 2) + xs_piece(b, ww >> 2) * 4 + (ww & 3)] = (uint32_t)v[k];
+      for (int k = 0; k < NB; k++) {
+        const int w = k0 + k, m = w >> 1, b = m / WPR2, ww = 512 * (m % WPR2) + 2 * t + (w & 1);
+        dst[b * (K / 2) + xs_piece(b, ww >> 2) * 4 + (ww & 3)] = (uint32_t)v[k];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k0 = 0; k0 < PER; k0 += NB) {
+      uint64_t v[NB];
+      ok = ok && poll_tagged<NB>([&](int k) { return src + t + 256 * (k0 + k); }, v, tag, c.ws);
+      if (k0 == 0) p4_trace_poll(c);
+#pragma unroll
+      for (int k = 0; k < NB; k++) {
+        // word t + 256 m of [B][K/2]: row m / WPR, word 256 (m % WPR) + t of it,
+        // its 16-byte piece XOR-swizzled by the row (xs_piece)
+        constexpr int WPR = K / 2 / 256;
+        const int m = k0 + k, b = m / WPR, ww = 256 * (m % WPR) + t;
+        dst[b * (K / 2) + xs_piece(b, ww >> 2) * 4 + (ww & 3)] = (uint32_t)v[k];
+      }
     }
   }
   return p4_agree(c, ok);
@@ -368,20 +417,24 @@ __device__ __forceinline__ bool p4_stage_norm(const MkdStepDesc& d, const P4& c,
   } else if (rk.valid) {
     // hidden words only: rows in groups of GH (2 words each)
     constexpr int GH = B < 4 ? B : 4;  // (8 at batch 8: +54 us, measured)
+    // this thread's words 2 t, 2 t + 1 of each row: one 16-byte load per row
+    // (batch 1 -3 us, batch 4 -7, batch 8 -13, C4 -13, C5 batch 8 -14)
+    const __amdgpu_buffer_rsrc_t hrs = pair_rsrc(c.ws.tw(hid + (size_t)c.rep * TW_GROUP));
     auto haddr = [&](int b0) {
-      return [=](int k) { return c.ws.tw(hid + (size_t)c.rep * TW_GROUP + (size_t)(b0 + (k >> 1)) * (H / 2) + 2 * t + (k & 1)); };
+      return [=](int k) { return PairAddr{hrs, (uint32_t)(16 * ((b0 + (k >> 1)) * (H / 4) + t))}; };
     };
+    constexpr bool PR = true;
     uint64_t first[2 * GH];
-    poll_issue<2 * GH>(haddr(0), first);  // before any other load of this task
+    poll_round<2 * GH, PR>(haddr(0), first);  // before any other load of this task
     wv = load_nw();
 #pragma unroll
     for (int b0 = 0; b0 < B; b0 += GH) {
       uint64_t v[2 * GH];
       if (b0 == 0) {
-        ok = poll_finish<2 * GH>(haddr(0), first, v, tag_in, c.ws);
+        ok = poll_finish<2 * GH, PR>(haddr(0), first, v, tag_in, c.ws);
         p4_trace_poll(c);
       } else {
-        ok = ok && poll_tagged<2 * GH>(haddr(b0), v, tag_in, c.ws);
+        ok = ok && poll_tagged<2 * GH, PR>(haddr(b0), v, tag_in, c.ws);
       }
 #pragma unroll
       for (int g = 0; g < GH; g++) {
