@@ -318,8 +318,10 @@ __device__ __forceinline__ bool p4_stage_copy(const P4& c, size_t base, uint32_t
   // the most words per hand-over: down input 48 words per thread in two groups
   // of 24, o_proj input 32 in two of 16 (measured against 12 / 8: batch 8
   // -21 us, C4 -24 us; one group of 48 or 32: +150 / +65 us, register bound).
-  // Larger groups at batch 2 and 4 measured no faster.
-  constexpr int NB = B >= 8 && K == 3072 ? 24 : (B >= 8 && K == 2048 ? 16 : largest_divisor_le8(PER));
+  // Batch 4's down input in two groups of 12 (with the paired loads below:
+  // -4.6 us against three of 8); o_proj's in one of 16 measured +19 us and
+  // larger groups at batch 2 no faster.
+  constexpr int NB = K == 3072 && B >= 4 ? 3 * B : (B >= 8 && K == 2048 ? 16 : largest_divisor_le8(PER));
   static_assert(PER % NB == 0, "whole groups");
   const int t = p4_tid();
   const uint64_t* src = c.ws.tw(base + (size_t)c.rep * TW_GROUP);
